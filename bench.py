@@ -1,0 +1,162 @@
+#!/usr/bin/env python3
+"""Benchmark of the shard commitment hot path on one MI355X.
+
+One step = one commitment of the resident input: coset/subgroup LDE (blowup
+4), the Poseidon2 Merkle tree over the codeword rows (root read back), and
+one fold round (k = 4) over the codeword, on 2^24 rows x 16 columns of
+uniform Goldilocks elements (2^28 input elements). Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+                  [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+METRIC = "committed Goldilocks elems/sec (LDE+Merkle) at 2^24x16, % HBM roofline"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=1 << 16,
+                    help="coefficient rows of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def cpu_baseline(wl, rows: int):
+    """The oracle (C restatement of the reference CPU path) on a bounded
+    sample of the same workload, all host cores (OpenMP)."""
+    from oracle import oracle as O
+    from zkie_amd import configs as C
+
+    threads = min(os.cpu_count() or 1, 16)
+    O.set_threads(threads)
+    sample = wl.scaled(rows)
+    data = O.gen_uniform(C.SEED_DATA, sample.elems).reshape(sample.rows, sample.cols)
+    ch = C.challenges(wl.fold_k) if wl.fold_k else None
+    t0 = time.perf_counter()
+    cw = O.lde_batch(data, sample.log_blowup)
+    _, root = O.merkle_commit(cw)
+    if ch is not None:
+        O.fold_rows(cw, wl.fold_k, ch, False)
+    dt = time.perf_counter() - t0
+    return {
+        "value": sample.elems / dt,
+        "unit": "elem/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample.rows} rows x {sample.cols} cols, blowup {1 << sample.log_blowup}, "
+                  f"LDE + Merkle root + fold k={wl.fold_k}; {dt:.2f} s wall",
+    }
+
+
+def leaf_traffic_bytes():
+    """HBM bytes per p2_leaf launch measured with rocprofv3 (FETCH_SIZE +
+    WRITE_SIZE, copy-kernel scaled), from the committed profile summary."""
+    path = os.path.join(ROOT, "profiles", "p2_leaf_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the multi-GPU "
+              "sharding of this path is a design, not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+
+    from zkie_amd import _native as N
+    from zkie_amd import configs as C
+    from zkie_amd.pcs import HipMerkleTreeMmcs, fold_rows_device, lde_device
+    from zkie_amd._native import DeviceBuffer
+
+    wl = C.CONFIGS[args.config]
+    assert N.device_count() >= 1, "no HIP device"
+    data = N.gen_inputs(C.SEED_DATA, wl.elems, wl.kind)
+    d_in = DeviceBuffer.from_array(data)
+    del data
+    n, w = wl.codeword_rows, wl.cols
+    d_cw = DeviceBuffer(n * w)
+    lens = N.merkle_layout(n)
+    d_layers = DeviceBuffer(sum(lens) * 8)
+    d_fold = DeviceBuffer(2 * n) if wl.fold_k else None
+    ch = C.challenges(wl.fold_k) if wl.fold_k else None
+    mmcs = HipMerkleTreeMmcs()
+    L = N.load()
+    import numpy as np
+    root = np.zeros(8, np.uint64)
+
+    def step():
+        lde_device(d_in, wl.rows, w, wl.log_blowup, d_cw)
+        N.check(L.zkie_merkle_commit(d_cw.addr, n, w, d_layers.addr, N.p(root), None), "commit")
+        if wl.fold_k:
+            fold_rows_device(d_cw, n, wl.fold_k, ch, False, d_fold)
+
+    for _ in range(args.warmup):
+        step()
+    N.check(L.zkie_device_synchronize(), "sync")
+    N.profile_enable(True)
+    N.profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    N.check(L.zkie_device_synchronize(), "sync")
+    t = (time.perf_counter() - t0) / args.steps
+    per_kernel = {k: N.profile_query(k) for k in N.profile_names()}
+    N.profile_enable(False)
+
+    value = wl.elems / t
+    # Dominant kernel: the Merkle leaf hash (2 of the 3 permutations per row).
+    leaf_n, leaf_ms = per_kernel.get("p2_leaf", (0, 0.0))
+    leaf_avg_ms = leaf_ms / max(leaf_n, 1)
+    leaf_alg_bytes = n * w * 8 + n * 64       # read the codeword rows, write layer-0 digests
+    achieved = leaf_alg_bytes / (leaf_avg_ms * 1e-3) / 1e9 if leaf_avg_ms else 0.0
+    traffic = leaf_traffic_bytes()
+    stage_ms = {k: round(ms / max(cnt, 1) * max(cnt, 1) / args.steps, 3) for k, (cnt, ms) in per_kernel.items()}
+    # whole-step HBM floor: 8 B in + 32 B codeword + 32 B digests (+ 36 B fold) per input element
+    step_alg_bytes = wl.elems * (72 + (36 if wl.fold_k else 0))
+
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "elem/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": t * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {"workload": f"config{wl.number}: {wl.name}", "rows": wl.rows, "cols": wl.cols,
+                   "log_blowup": wl.log_blowup, "fold_k": wl.fold_k,
+                   "codeword_rows": n, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "kernel": "p2_leaf", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic, "avg_ms": leaf_avg_ms},
+        "step_hbm_frac": step_alg_bytes / t / 1e9 / HBM_PEAK_GBS,
+        "stage_ms_per_step": stage_ms,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

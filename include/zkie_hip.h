@@ -1,0 +1,176 @@
+/*
+ * zkie_hip.h — C ABI of the MI355X (gfx950) shard-commitment library
+ * (libzkie_hip.so): coset/subgroup LDE over Goldilocks, Poseidon2 Merkle
+ * commitment with openings, and the WHIR/FRI row fold.
+ *
+ * Conventions (same as the reference FFI, crates/zkie-core/src/pcs/cuda_ffi.rs):
+ *  - every function returns int: 0 on success, a hipError_t value when the
+ *    HIP runtime fails, or a negative ZKIE_ERR_* code for bad arguments. The
+ *    library never falls back to a CPU path; callers that want one keep it on
+ *    their side, as dft_cuda.rs:174-177 and merkle_cuda.rs:328-335 do;
+ *  - matrices are row-major u64 arrays of canonical Goldilocks elements
+ *    (p = 2^64 - 2^32 + 1), digests are 8 contiguous u64, digest layers are
+ *    stored back to back ([layer0 | layer1 | ... | root]);
+ *  - pointers named d_* are device pointers owned by the caller; other
+ *    pointers are host memory;
+ *  - `stream` is a hipStream_t (NULL = the null stream). Entry points that
+ *    return host data synchronise that stream before returning.
+ *
+ * Reference paths are relative to the zkIE repository root.
+ */
+#ifndef ZKIE_HIP_H
+#define ZKIE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZKIE_OK 0
+#define ZKIE_ERR_INVALID (-1)     /* argument out of range or inconsistent */
+#define ZKIE_ERR_NO_DEVICE (-2)   /* no HIP device */
+#define ZKIE_ERR_ALLOC (-3)       /* device workspace allocation failed */
+
+/* ------------------------------------------------------------------------
+ * Device and memory. Replace the raw CUDA runtime imports of
+ * crates/zkie-core/src/pcs/cuda_ffi.rs:41-45 (cudaMalloc, cudaFree,
+ * cudaMemcpy, cudaDeviceSynchronize, cudaMemset) and the device count of
+ * crates/zkie-core/cuda/poseidon2_merkle.cu:315-318 (zkie_cuda_device_count).
+ * ---------------------------------------------------------------------- */
+int zkie_device_count(void);
+int zkie_dev_alloc(void **d_ptr, size_t bytes);
+int zkie_dev_free(void *d_ptr);
+int zkie_memcpy_htod(void *d_dst, const void *src, size_t bytes);
+int zkie_memcpy_dtoh(void *dst, const void *d_src, size_t bytes);
+int zkie_memcpy_dtod(void *d_dst, const void *d_src, size_t bytes, void *stream);
+int zkie_memset(void *d_ptr, int value, size_t bytes);
+int zkie_device_synchronize(void);
+int zkie_stream_synchronize(void *stream);
+
+/* ------------------------------------------------------------------------
+ * Reference-compatible kernels (same names, arguments and semantics as
+ * crates/zkie-core/src/pcs/cuda_ffi.rs:2-39).
+ * ---------------------------------------------------------------------- */
+
+/* goldilocks_ntt.cu:105-137. Forward DFT of every column of the row-major
+ * h x w matrix d_mat (h = 2^lg_h), in place, natural order in and out, on
+ * TWO_ADIC_GENERATORS[lg_h]; d_temp is caller scratch of h*w u64. d_tw is
+ * accepted for ABI compatibility and may be NULL: the library generates the
+ * identical twiddles itself (dft_cuda.rs:44-59) and has no 2^18 size cap. */
+int zkie_ntt_forward_goldilocks(uint64_t *d_mat, uint64_t *d_temp, uint32_t lg_h, uint64_t w,
+                                const uint64_t *d_tw);
+
+/* poseidon2_merkle.cu:252-264. rc_init/rc_final: 4 rounds x 16 host u64 each,
+ * rc_internal: 22 host u64, diag15: MATRIX_DIAG_16_GOLDILOCKS[15]. Applies to
+ * the current device; every later hashing entry point uses them. */
+int zkie_p2_upload_constants(const uint64_t *rc_init, const uint64_t *rc_final,
+                             const uint64_t *rc_internal, uint64_t diag15);
+
+/* poseidon2_merkle.cu:266-275: leaf digests of rows [0, 8*floor(h/8)). */
+int zkie_p2_leaf_batch(const uint64_t *d_mat, uint64_t *d_digests, uint32_t h, uint32_t w);
+/* poseidon2_merkle.cu:277-287: leaf digests of rows [start_row, h). */
+int zkie_p2_leaf_scalar(const uint64_t *d_mat, uint64_t *d_digests, uint32_t start_row,
+                        uint32_t h, uint32_t w);
+/* poseidon2_merkle.cu:289-299: parents [0, 8*floor(next_len/8)) of `step`
+ * children each (TruncatedPermutation<Perm, 2, 8, 16>). */
+int zkie_p2_compress_batch(const uint64_t *d_prev, uint64_t *d_next, uint32_t next_len,
+                           uint32_t step);
+/* poseidon2_merkle.cu:301-311: parents [from, to). */
+int zkie_p2_compress_scalar(const uint64_t *d_prev, uint64_t *d_next, uint32_t from,
+                            uint32_t to, uint32_t step);
+
+/* ------------------------------------------------------------------------
+ * Device-resident path. The codeword and the digest layers stay in HBM
+ * between stages, unlike the reference's per-stage H2D/D2H round trips
+ * (dft_cuda.rs:203,213; merkle_cuda.rs:227,288-306).
+ * ---------------------------------------------------------------------- */
+
+/* merkle_cuda.rs:54-85 (derive_poseidon2_constants): the constants of
+ * Poseidon2Goldilocks<16>::new_from_rng_128(SmallRng::seed_from_u64(1)),
+ * derived on the host; pass them to zkie_p2_upload_constants. The library
+ * uploads them by itself on first use when the caller never did. */
+int zkie_p2_default_constants(uint64_t rc_init[64], uint64_t rc_final[64],
+                              uint64_t rc_internal[22], uint64_t *diag15);
+
+/* TwoAdicSubgroupDft::dft_batch (dft_cuda.rs:161-222, contract at
+ * goldilocks_ntt.cu:3-23), in place on the device, any lg_h <= 32. */
+int zkie_dft_batch(uint64_t *d_mat, uint32_t lg_h, uint64_t w, void *stream);
+/* Inverse of zkie_dft_batch (evaluations -> coefficients), in place. */
+int zkie_idft_batch(uint64_t *d_mat, uint32_t lg_h, uint64_t w, void *stream);
+/* WHIR encode (p3-whir src/pcs/committer/writer.rs:73-81, Suffix order) and
+ * coset LDE: treat the h x w matrix d_in as coefficient rows, zero-pad it to
+ * n = h << log_blowup rows, scale row j by shift^j (shift = 1 is the
+ * reference's plain subgroup encode), and write the n x w evaluations to
+ * d_out. h must be a power of two. d_in and d_out must not overlap. */
+int zkie_lde_batch(const uint64_t *d_in, uint64_t h, uint64_t w, uint32_t log_blowup,
+                   uint64_t shift, uint64_t *d_out, void *stream);
+
+/* Tree geometry of MerkleTree::new for one matrix of height h, arity 2
+ * (p3-merkle-tree merkle_tree.rs:95-178, padded_len at :577-585; the same
+ * schedule as merkle_cuda.rs:203-209). layer_lens must hold 65 entries. */
+int zkie_merkle_layout(uint64_t h, uint32_t *num_layers, uint64_t *layer_lens);
+/* Mmcs::commit for one matrix (merkle_cuda.rs:177-312, mmcs/batch.rs:42-64):
+ * hash every row of the h x w matrix d_mat with PaddingFreeSponge<Perm,16,8,8>,
+ * compress layer by layer, zero digests in padded slots. d_layers holds
+ * sum(layer_lens) * 8 u64. root (host, 8 u64, may be NULL) receives the cap
+ * (cap height 0). */
+int zkie_merkle_commit(const uint64_t *d_mat, uint64_t h, uint64_t w, uint64_t *d_layers,
+                       uint64_t *root, void *stream);
+/* Mmcs::open_batch (p3-merkle-tree mmcs/batch.rs:75-121) for n indices at
+ * once: rows_out (host, n*w u64) receives the opened rows, siblings_out
+ * (host, n*(num_layers-1)*8 u64) the authentication paths, bottom-up. */
+int zkie_merkle_open_batch(const uint64_t *d_mat, uint64_t h, uint64_t w,
+                           const uint64_t *d_layers, const uint64_t *indices, uint64_t n,
+                           uint64_t *rows_out, uint64_t *siblings_out, void *stream);
+/* Mmcs::open_multi_batch / open_batch_pruned (p3-merkle-tree mmcs/mod.rs:309-461,
+ * pruning.rs:130-232): rows_out as above (input order), pruned_out (host,
+ * capacity `cap` digests) the boundary siblings in frontier order; *count is
+ * the number of digests of the proof (may exceed cap, then nothing past cap
+ * is written and ZKIE_ERR_INVALID is returned). */
+int zkie_merkle_open_pruned(const uint64_t *d_mat, uint64_t h, uint64_t w,
+                            const uint64_t *d_layers, const uint64_t *indices, uint64_t n,
+                            uint64_t *rows_out, uint64_t *pruned_out, uint64_t cap,
+                            uint64_t *count, void *stream);
+
+/* Row fold of the WHIR prover (p3-whir src/pcs/prover/mod.rs:257-290, equal to
+ * zkIE's mle::eval at common/mle.rs:8-22 with variable 0 the least-significant
+ * index bit): out[t] = sum_j eq(r, j) * row_t[j] over the 2^log_width entries
+ * of each of the h rows. Rows are base elements (is_ext = 0, 2^log_width u64)
+ * or EF = F[x]/(x^2 - 7) elements flattened [c0, c1] (is_ext = 1). r (host)
+ * holds log_width EF challenges (2*log_width u64); d_out receives h EF
+ * elements (2h u64). log_width <= 8. */
+int zkie_fold_rows(const uint64_t *d_mat, uint64_t h, uint32_t log_width, int is_ext,
+                   const uint64_t *r, uint64_t *d_out, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Synthetic inputs (host): XorShift64 of common/field.rs:17-36 seeded with
+ * `seed`, embedded like common/fixed_point.rs:11-38. ZKIE_GEN_UNIFORM:
+ * next_u64() mod p; ZKIE_GEN_I16: (next_u64() % 65536) as i16;
+ * ZKIE_GEN_I8: (next_u64() % 255) - 127; ZKIE_GEN_GAUSS_I16: integer
+ * Irwin-Hall N(0,1) (sum of 12 next_u64() >> 11, scaled 2^-53, minus 6)
+ * times 0.02 * 2^12, rounded half up, clamped to int16.
+ * ---------------------------------------------------------------------- */
+#define ZKIE_GEN_UNIFORM 0
+#define ZKIE_GEN_I16 1
+#define ZKIE_GEN_I8 2
+#define ZKIE_GEN_GAUSS_I16 3
+int zkie_gen_inputs(uint64_t seed, uint64_t n, int kind, uint64_t *out);
+
+/* ------------------------------------------------------------------------
+ * Kernel timers (no reference counterpart; stands in for the per-Whir
+ * commit_stats counters of whir.rs:270-273,361-370). When enabled, each
+ * kernel launch is bracketed by HIP events on its own stream.
+ * ---------------------------------------------------------------------- */
+int zkie_profile_enable(int on);
+int zkie_profile_reset(void);
+/* Totals for one kernel name since the last reset (synchronises the device). */
+int zkie_profile_query(const char *kernel, uint64_t *launches, double *total_ms);
+/* Newline-separated kernel names seen since the last reset. */
+int zkie_profile_names(char *buf, size_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZKIE_HIP_H */

@@ -1,0 +1,122 @@
+// CPU emulation of the device code of libzkie_hip.so (test infrastructure).
+//
+// Built host-only from the same headers the kernels use, with the device
+// 32-bit-limb multiply (ZK_LIMB_MUL_ON_HOST) and bounds checks on every
+// global and LDS access (ZK_EMU_BOUNDS). Each NTT pass is executed phase by
+// phase for every thread of every workgroup, in the order the barriers
+// impose, so index mistakes abort here instead of faulting a GPU.
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "../../zkie_amd/csrc/ntt_plan.hpp"
+#include "../../zkie_amd/csrc/poseidon2.hpp"
+
+using namespace zk;
+
+namespace {
+
+void run_pass(const PassArgs& a, uint32_t T)
+{
+    const uint64_t blocks = pass_blocks(a);
+    std::vector<uint64_t> lds((size_t)1 << (a.s + a.logC + a.logJ));
+    for (uint64_t bid = 0; bid < blocks; bid++) {
+        const PassTile t = pass_tile(a, bid);
+        if (t.E != lds.size()) std::abort();
+        for (uint32_t tid = 0; tid < T; tid++) pass_load(a, t, tid, T, lds.data());
+        for (int lm = (int)a.s - 1; lm >= 0; lm--)
+            for (uint32_t tid = 0; tid < T; tid++) pass_stage(a, t, lm, tid, T, lds.data());
+        for (uint32_t tid = 0; tid < T; tid++) pass_store(a, t, tid, T, lds.data());
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t emu_gl_add(uint64_t a, uint64_t b) { return gl_add(a, b); }
+uint64_t emu_gl_sub(uint64_t a, uint64_t b) { return gl_sub(a, b); }
+uint64_t emu_gl_mul(uint64_t a, uint64_t b) { return gl_mul(a, b); }
+uint64_t emu_gl_sqr(uint64_t a) { return gl_sqr(a); }
+uint64_t emu_gl_halve(uint64_t a) { return gl_halve(a); }
+uint64_t emu_gl_inv_pow2(uint64_t a, int k)
+{
+    switch (k) {
+        case 3: return gl_mul_inv_pow2<3>(a);
+        case 4: return gl_mul_inv_pow2<4>(a);
+        case 5: return gl_mul_inv_pow2<5>(a);
+        case 32: return gl_mul_inv_pow2<32>(a);
+        default: return 0;
+    }
+}
+uint64_t emu_acc_sum(const uint64_t* x, uint64_t n)
+{
+    Acc a = acc_of(0);
+    for (uint64_t i = 0; i < n; i++) a = acc_add(a, x[i]);
+    return acc_reduce(a);
+}
+uint64_t emu_gl_canon(uint64_t a) { return gl_canon(a); }
+
+// Permutation with explicit constants (layout of zkie_p2_upload_constants).
+void emu_p2_permute(uint64_t* st, const uint64_t* rc_init, const uint64_t* rc_final,
+                    const uint64_t* rc_internal, uint64_t diag15, int fast_diag)
+{
+    P2Consts c;
+    for (int k = 0; k < 4; k++)
+        for (int i = 0; i < 16; i++) {
+            c.ext[k][i] = rc_init[16 * k + i];
+            c.ext[4 + k][i] = rc_final[16 * k + i];
+        }
+    for (int k = 0; k < 22; k++) c.internal[k] = rc_internal[k];
+    c.diag15 = diag15;
+    if (fast_diag)
+        p2_permute<true>(st, c);
+    else
+        p2_permute<false>(st, c);
+    for (int i = 0; i < 16; i++) st[i] = gl_canon(st[i]);
+}
+
+// DFT (in place) / LDE through the device pass code. Returns 0 on success.
+int emu_dft(uint64_t* mat, uint32_t lg, uint64_t w, int inverse, uint32_t threads)
+{
+    if (lg == 0 || w == 0) return 0;
+    const std::vector<uint64_t> tab = build_twiddle_tables();
+    const Plan p = make_plan(lg, w);
+    const uint64_t n = 1ull << lg;
+    std::vector<uint64_t> tmp(n * w);
+    uint32_t B = lg;
+    for (uint32_t i = 0; i < p.np; i++) {
+        PassArgs a = pass_args(p, i, B, w, mat, n, tmp.data(), p.np == 1 ? mat : mat, tab.data(), inverse != 0);
+        if (p.np == 1) {
+            // single pass in place: emulate the load-all-then-store order
+            std::vector<uint64_t> src(mat, mat + n * w);
+            a.in = src.data();
+            run_pass(a, threads);
+        } else {
+            run_pass(a, threads);
+        }
+        B -= a.s;
+    }
+    return 0;
+}
+
+int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t* out,
+            uint32_t threads)
+{
+    uint32_t lgh = 0;
+    while ((1ull << lgh) < h) lgh++;
+    const uint32_t L = lgh + log_blowup;
+    const std::vector<uint64_t> tab = build_twiddle_tables();
+    const Plan p = make_plan(L, w);
+    const uint64_t n = 1ull << L;
+    std::vector<uint64_t> tmp(n * w);
+    uint32_t B = L;
+    for (uint32_t i = 0; i < p.np; i++) {
+        const PassArgs a = pass_args(p, i, B, w, in, h, tmp.data(), out, tab.data(), false);
+        run_pass(a, threads);
+        B -= a.s;
+    }
+    return 0;
+}
+
+}  // extern "C"

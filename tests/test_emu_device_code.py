@@ -1,0 +1,67 @@
+"""The device code of libzkie_hip.so, built for the host (tests/emu/emu.cpp),
+checked against the oracle: the 32-bit-limb Goldilocks arithmetic on edge
+and non-canonical values, the permutation in both diagonal modes, and the NTT
+pass kernels (every workgroup and thread executed with bounds checks)."""
+import random
+
+import numpy as np
+import pytest
+
+from tests.emu.emu import ptr
+
+P = 0xFFFFFFFF00000001
+M = (1 << 64) - 1
+EDGE = [0, 1, 2, P - 1, P, P + 1, M, M - 1, 2**32 - 1, 2**32, 2**63, P - 2**32, 2**64 - 2**32]
+
+
+def test_arithmetic(emu):
+    rng = random.Random(1)
+    vals = EDGE + [rng.getrandbits(64) for _ in range(4000)]
+    for a in vals:
+        b = rng.choice(vals)
+        assert emu.emu_gl_canon(emu.emu_gl_add(a, b)) == (a + b) % P
+        assert emu.emu_gl_canon(emu.emu_gl_sub(a, b)) == (a - b) % P
+        assert emu.emu_gl_canon(emu.emu_gl_mul(a, b)) == (a * b) % P
+        assert emu.emu_gl_canon(emu.emu_gl_sqr(a)) == (a * a) % P
+        assert emu.emu_gl_canon(emu.emu_gl_halve(a)) == a * pow(2, P - 2, P) % P
+        for k in (3, 4, 5, 32):
+            assert emu.emu_gl_canon(emu.emu_gl_inv_pow2(a, k)) == a * pow(2**k, P - 2, P) % P
+    for n in (1, 16, 36, 1000):
+        x = np.array([rng.getrandbits(64) for _ in range(n)], np.uint64)
+        assert emu.emu_gl_canon(emu.emu_acc_sum(ptr(x), n)) == sum(int(v) for v in x) % P
+
+
+@pytest.mark.parametrize("fast", [0, 1])
+def test_permutation(emu, oracle, fast):
+    a, b, c, d = oracle.p2_constants()
+    rng = random.Random(2 + fast)
+    for _ in range(30):
+        st = np.array([rng.getrandbits(64) % P for _ in range(16)], np.uint64)
+        ref = oracle.p2_permute(st)
+        s = st.copy()
+        emu.emu_p2_permute(ptr(s), ptr(a), ptr(b), ptr(c), d, fast)
+        assert (s == ref).all()
+    # non-canonical inputs (values in [p, 2^64)) reduce to the same result
+    st = np.array([P + i for i in range(16)], np.uint64)
+    s = st.copy()
+    emu.emu_p2_permute(ptr(s), ptr(a), ptr(b), ptr(c), d, fast)
+    assert (s == oracle.p2_permute(np.arange(16, dtype=np.uint64))).all()
+
+
+@pytest.mark.parametrize("lg,w", [(1, 1), (3, 1), (5, 3), (9, 16), (10, 1), (10, 16), (12, 5),
+                                  (14, 32), (16, 8), (19, 1), (18, 16), (13, 128)])
+def test_dft_passes(emu, oracle, lg, w):
+    x = oracle.gen_uniform(lg * 100 + w, (1 << lg) * w).reshape(1 << lg, w)
+    y = x.copy()
+    assert emu.emu_dft(ptr(y), lg, w, 0, 256) == 0
+    assert (y == oracle.dft_batch(x)).all()
+    assert emu.emu_dft(ptr(y), lg, w, 1, 256) == 0
+    assert (y == x).all()
+
+
+@pytest.mark.parametrize("lg,w,lb", [(4, 1, 2), (10, 16, 2), (16, 1, 2), (9, 32, 3), (12, 16, 1)])
+def test_lde_passes(emu, oracle, lg, w, lb):
+    x = oracle.gen_uniform(7, (1 << lg) * w).reshape(1 << lg, w)
+    out = np.zeros(((1 << lg) << lb, w), np.uint64)
+    assert emu.emu_lde(ptr(x), 1 << lg, w, lb, ptr(out), 256) == 0
+    assert (out == oracle.lde_batch(x, lb)).all()

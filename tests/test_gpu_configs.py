@@ -1,0 +1,142 @@
+"""The five workloads on the GPU against the oracle.
+
+Configs 1, 2 and 5 are compared bit for bit at their full sizes (codewords,
+every digest layer, roots, folded tables, openings). Configs 3 and 4 are
+compared bit for bit on scaled-down shapes that take the same kernel paths,
+and at full size through size-independent properties: the inverse DFT of the
+codeword returns the zero-padded input, sampled codeword entries equal direct
+polynomial evaluation, sampled digests equal the oracle hash of their
+children, sampled opening paths verify against the root, and sampled folded
+entries equal the oracle fold of their rows."""
+import numpy as np
+import pytest
+
+from zkie_amd import configs as C
+from zkie_amd import pipeline as PL
+from zkie_amd._native import DeviceBuffer, check
+
+pytestmark = pytest.mark.gpu
+
+P = 0xFFFFFFFF00000001
+
+
+def _case(*a):
+    print("CASE", *a, flush=True)
+
+
+def oracle_workload(O, wl: C.Workload, data: np.ndarray):
+    """The same pipeline composed from oracle functions."""
+    res = {"rounds": [], "fold": None, "tables": []}
+    cw = O.lde_batch(data, wl.log_blowup)
+    layers, root = O.merkle_commit(cw)
+    res["rounds"].append((cw, layers, root))
+    k = wl.fold_k
+    if k and wl.rounds == 0:
+        res["fold"] = O.fold_rows(cw, k, C.challenges(k), False)
+    if wl.rounds:
+        ch = C.challenges(k * wl.rounds)
+        table, ext = data, False
+        for r in range(wl.rounds):
+            folded = O.fold_rows(table, k, ch[k * r:k * (r + 1)], ext)  # (rows, 2)
+            res["tables"].append(folded)
+            coeff = folded.reshape(-1, 2 << k)
+            cw = O.lde_batch(coeff, wl.log_blowup)
+            layers, root = O.merkle_commit(cw)
+            res["rounds"].append((cw, layers, root))
+            table, ext = coeff, True
+    return res
+
+
+def compare_full(O, wl, data, out, ref):
+    assert len(out.rounds) == len(ref["rounds"])
+    g = C.XorShift64(C.SEED_QUERIES)
+    for rnd, (cw, layers, root) in zip(out.rounds, ref["rounds"]):
+        assert (rnd.codeword.download().reshape(cw.shape) == cw).all()
+        got = rnd.tree.layers()
+        assert len(got) == len(layers)
+        for a, b in zip(got, layers):
+            assert (a == b).all()
+        assert (rnd.tree.root == root).all()
+        if wl.queries:
+            idx = C.query_indices(wl.queries, rnd.rows, g)
+            assert (rnd.queries == idx).all()
+            assert (rnd.opened_rows == cw[idx.astype(np.int64)]).all()
+            for k, i in enumerate(idx):
+                assert (rnd.paths[k] == O.merkle_open(layers, rnd.rows, int(i))).all()
+                assert O.merkle_verify(root, rnd.rows, int(i), rnd.opened_rows[k], rnd.paths[k])
+            assert (rnd.pruned == O.merkle_open_pruned(layers, rnd.rows, idx)).all()
+    if ref["fold"] is not None:
+        assert (out.fold.download().reshape(-1, 2) == ref["fold"]).all()
+    for (buf, n), t in zip(out.tables, ref["tables"]):
+        assert (buf.download().reshape(-1, 2) == t).all()
+
+
+@pytest.mark.parametrize("number,rows", [(1, None), (2, None), (5, None), (3, 1 << 18), (3, 1 << 10),
+                                         (4, 1 << 12), (5, 1 << 12)])
+def test_workload_bit_exact(native, oracle, number, rows):
+    wl = C.CONFIGS[number] if rows is None else C.CONFIGS[number].scaled(rows)
+    _case("workload", wl.name)
+    data = PL.workload_inputs(wl)
+    assert (data.reshape(-1) == {0: oracle.gen_uniform, 1: oracle.gen_i16, 2: oracle.gen_i8,
+                                 3: oracle.gen_gauss_i16}[wl.kind](C.SEED_DATA, wl.elems)).all()
+    d_in = DeviceBuffer.from_array(data)
+    out = PL.run_workload(wl, d_in)
+    ref = oracle_workload(oracle, wl, data)
+    compare_full(oracle, wl, data, out, ref)
+
+
+def property_checks(native, oracle, wl, data, out, rng, samples=24):
+    rnd = out.rounds[0]
+    n, w = rnd.rows, rnd.width
+    # 1) the inverse DFT of the whole codeword is the zero-padded input
+    lg = n.bit_length() - 1
+    chk = DeviceBuffer(n * w)
+    check(native.load().zkie_memcpy_dtod(chk.addr, rnd.codeword.addr, n * w * 8, None), "copy")
+    check(native.load().zkie_idft_batch(chk.addr, lg, w, None), "idft")
+    back = chk.download().reshape(n, w)
+    assert (back[: wl.rows] == data).all()
+    assert not back[wl.rows:].any()
+    del back, chk
+    # 2) sampled codeword entries = direct evaluation at w_n^t
+    g = oracle.two_adic_generator(lg)
+    for _ in range(3):
+        t, c = int(rng.integers(n)), int(rng.integers(w))
+        val = rnd.codeword.download(1, t * w + c)[0]
+        assert int(val) == oracle.poly_eval(data, c, pow(g, t, P))
+    # 3) sampled leaves and internal nodes against the oracle hash
+    offs, acc = [], 0
+    for ln in rnd.tree.layer_lens:
+        offs.append(acc)
+        acc += ln * 8
+    for _ in range(samples):
+        i = int(rng.integers(n))
+        row = rnd.codeword.download(w, i * w)
+        assert (rnd.tree.d_layers.download(8, offs[0] + 8 * i) == oracle.leaf_hash(row)).all()
+    for lvl in range(1, len(rnd.tree.layer_lens)):
+        for _ in range(4):
+            j = int(rng.integers(rnd.tree.layer_lens[lvl]))
+            kids = rnd.tree.d_layers.download(16, offs[lvl - 1] + 16 * j)
+            par = rnd.tree.d_layers.download(8, offs[lvl] + 8 * j)
+            assert (par == oracle.compress(kids[:8], kids[8:])).all()
+    # 4) opening paths verify against the root
+    idx = np.unique(rng.integers(0, n, size=samples).astype(np.uint64))
+    from zkie_amd.pcs import HipMerkleTreeMmcs
+    rows, paths = HipMerkleTreeMmcs().open_batches(idx, rnd.tree)
+    for k, i in enumerate(idx):
+        assert oracle.merkle_verify(rnd.tree.root, n, int(i), rows[k], paths[k])
+    # 5) sampled fold entries
+    if out.fold is not None:
+        ch = C.challenges(wl.fold_k)
+        for k, i in enumerate(idx[:8]):
+            got = out.fold.download(2, 2 * int(i))
+            assert (got == oracle.fold_rows(rows[k:k + 1], wl.fold_k, ch, False)[0]).all()
+
+
+@pytest.mark.parametrize("number", [3, 4])
+def test_workload_full_size_properties(native, oracle, number):
+    wl = C.CONFIGS[number]
+    _case("full-size properties", wl.name)
+    data = PL.workload_inputs(wl)
+    d_in = DeviceBuffer.from_array(data)
+    out = PL.run_workload(wl, d_in, with_openings=False)
+    property_checks(native, oracle, wl, data, out, np.random.default_rng(number))

@@ -1,0 +1,145 @@
+// WHIR/FRI row fold on MI355X.
+//
+// out[t] = sum_j eq(r, j) * row_t[j], eq(r, j) = prod_b (j_b ? r_b : 1 - r_b),
+// bit 0 the least-significant index bit. This is zkIE's mle::eval
+// (common/mle.rs:8-22) applied to every row, i.e. the codeword row fold of
+// the WHIR prover (p3-whir src/pcs/prover/mod.rs:257-290, Suffix order) and,
+// applied to the table viewed as 2^(n-k) rows of 2^k, the table fold over
+// the low k variables (mle.rs:25-38 partial_eval).
+// One row per lane; the 2^k eq weights are computed once on the host and
+// read as wave-uniform values; the codeword is streamed exactly once.
+#include <vector>
+
+#include "gl64.hpp"
+#include "runtime.hpp"
+
+namespace zk {
+namespace {
+
+template <int K, bool EXT>
+__global__ __launch_bounds__(256) void fold_kernel(const uint64_t* __restrict__ mat, uint64_t h,
+                                                   const uint64_t* __restrict__ eq,
+                                                   uint64_t* __restrict__ out)
+{
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= h) return;
+    constexpr int Wd = 1 << K;
+    Acc s0 = acc_of(0), s1 = acc_of(0);
+    if (!EXT) {
+        const ulonglong2* row = reinterpret_cast<const ulonglong2*>(mat + t * Wd);
+#pragma unroll
+        for (int j2 = 0; j2 < Wd / 2; j2++) {
+            const ulonglong2 x = row[j2];
+            s0 = acc_add(s0, gl_mul(eq[4 * j2 + 0], x.x));
+            s1 = acc_add(s1, gl_mul(eq[4 * j2 + 1], x.x));
+            s0 = acc_add(s0, gl_mul(eq[4 * j2 + 2], x.y));
+            s1 = acc_add(s1, gl_mul(eq[4 * j2 + 3], x.y));
+        }
+    } else {
+        const ulonglong2* row = reinterpret_cast<const ulonglong2*>(mat + t * 2 * Wd);
+#pragma unroll
+        for (int j = 0; j < Wd; j++) {
+            const ulonglong2 y = row[j];
+            const uint64_t e0 = eq[2 * j], e1 = eq[2 * j + 1];
+            s0 = acc_add(s0, gl_mul(e0, y.x));
+            s0 = acc_add(s0, gl_mul7(gl_mul(e1, y.y)));
+            s1 = acc_add(s1, gl_mul(e0, y.y));
+            s1 = acc_add(s1, gl_mul(e1, y.x));
+        }
+    }
+    reinterpret_cast<ulonglong2*>(out)[t] = make_ulonglong2(gl_canon(acc_reduce(s0)), gl_canon(acc_reduce(s1)));
+}
+
+// Generic width (K > 6): runtime loop.
+template <bool EXT>
+__global__ __launch_bounds__(256) void fold_kernel_rt(const uint64_t* __restrict__ mat, uint64_t h,
+                                                      uint32_t k, const uint64_t* __restrict__ eq,
+                                                      uint64_t* __restrict__ out)
+{
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= h) return;
+    const uint64_t Wd = 1ull << k;
+    uint64_t s0 = 0, s1 = 0;
+    for (uint64_t j = 0; j < Wd; j++) {
+        const uint64_t e0 = eq[2 * j], e1 = eq[2 * j + 1];
+        if (!EXT) {
+            const uint64_t x = mat[t * Wd + j];
+            s0 = gl_add(s0, gl_mul(e0, x));
+            s1 = gl_add(s1, gl_mul(e1, x));
+        } else {
+            const uint64_t y0 = mat[(t * Wd + j) * 2], y1 = mat[(t * Wd + j) * 2 + 1];
+            s0 = gl_add(s0, gl_add(gl_mul(e0, y0), gl_mul7(gl_mul(e1, y1))));
+            s1 = gl_add(s1, gl_add(gl_mul(e0, y1), gl_mul(e1, y0)));
+        }
+    }
+    out[2 * t] = gl_canon(s0);
+    out[2 * t + 1] = gl_canon(s1);
+}
+
+// eq table on the host: eq[j] = prod_b (bit_b(j) ? r_b : 1 - r_b) (mle.rs:44-56).
+std::vector<uint64_t> eq_table(const uint64_t* r, uint32_t k)
+{
+    const uint64_t n = 1ull << k;
+    std::vector<Ef> e(n, Ef{1, 0});
+    for (uint32_t b = 0; b < k; b++) {
+        const Ef rb{gl_canon(r[2 * b]), gl_canon(r[2 * b + 1])};
+        const Ef one_minus = ef_sub(Ef{1, 0}, rb);
+        for (uint64_t j = 0; j < n; j++) e[j] = ef_mul(e[j], ((j >> b) & 1) ? rb : one_minus);
+    }
+    std::vector<uint64_t> flat(2 * n);
+    for (uint64_t j = 0; j < n; j++) {
+        flat[2 * j] = gl_canon(e[j].c0);
+        flat[2 * j + 1] = gl_canon(e[j].c1);
+    }
+    return flat;
+}
+
+}  // namespace
+
+int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const uint64_t* r,
+                uint64_t* d_out, hipStream_t s)
+{
+    if (k > 8 || !r || (h && (!d_mat || !d_out))) return ZKIE_ERR_INVALID;
+    if (h == 0) return ZKIE_OK;
+    const std::vector<uint64_t> eq = eq_table(r, k);
+    uint64_t* d_eq = (uint64_t*)workspace(WS_MISC, eq.size() * 8);
+    if (!d_eq) return ZKIE_ERR_ALLOC;
+    ZK_TRY(hipMemcpyAsync(d_eq, eq.data(), eq.size() * 8, hipMemcpyHostToDevice, s));
+    const unsigned grid = (unsigned)((h + 255) / 256);
+    ProfMark m = prof_begin("fold_rows", s);
+#define ZK_FOLD(KK)                                                                  \
+    case KK:                                                                         \
+        if (is_ext)                                                                  \
+            fold_kernel<KK, true><<<grid, 256, 0, s>>>(d_mat, h, d_eq, d_out);       \
+        else                                                                         \
+            fold_kernel<KK, false><<<grid, 256, 0, s>>>(d_mat, h, d_eq, d_out);      \
+        break;
+    switch (k) {
+        ZK_FOLD(1)
+        ZK_FOLD(2)
+        ZK_FOLD(3)
+        ZK_FOLD(4)
+        ZK_FOLD(5)
+        ZK_FOLD(6)
+        default:
+            if (is_ext)
+                fold_kernel_rt<true><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
+            else
+                fold_kernel_rt<false><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
+            break;
+    }
+#undef ZK_FOLD
+    prof_end(m, s);
+    ZK_LAUNCHED();
+    // The eq buffer is shared workspace: finish before a later call reuses it.
+    ZK_TRY(hipStreamSynchronize(s));
+    return ZKIE_OK;
+}
+
+}  // namespace zk
+
+extern "C" int zkie_fold_rows(const uint64_t* d_mat, uint64_t h, uint32_t log_width, int is_ext,
+                              const uint64_t* r, uint64_t* d_out, void* stream)
+{
+    return zk::fold_device(d_mat, h, log_width, is_ext, r, d_out, zk::as_stream(stream));
+}

@@ -1,0 +1,185 @@
+// Goldilocks arithmetic for CDNA4 (gfx950) and the host.
+//
+// p = 2^64 - 2^32 + 1, eps = 2^64 mod p = 2^32 - 1, 2^96 = -1 (mod p).
+// Device values live in [0, 2^64) and need not be canonical; every helper
+// accepts any u64 and returns a u64 congruent to the exact result. Only
+// `gl_canon` produces the canonical representative; every value that leaves
+// a kernel goes through it, so all outputs are canonical u64 exactly like the
+// reference ABI (goldilocks_ntt.cu:92, poseidon2_merkle.cu:183).
+//
+// The 64x64 product is built from four v_mad_u64_u32 (32x32+64 -> 64) and
+// reduced with the special form of p; there is no MFMA path here because
+// nothing in this field is a dense float contraction. Defining
+// ZK_LIMB_MUL_ON_HOST makes host builds run the same 32-bit-limb product
+// (used by the CPU emulation tests of the device code).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zk {
+
+constexpr uint64_t P = 0xFFFFFFFF00000001ull;
+constexpr uint64_t EPS = 0xFFFFFFFFull;
+constexpr uint64_t HALF = 0x7FFFFFFF80000001ull;  // (p + 1) / 2
+constexpr uint64_t INV_2_32 = 0xFFFFFFFE00000002ull;  // 2^-32 mod p
+
+__host__ __device__ __forceinline__ uint64_t gl_canon(uint64_t a) { return a >= P ? a - P : a; }
+
+// a + b for any a, b < 2^64.
+__host__ __device__ __forceinline__ uint64_t gl_add(uint64_t a, uint64_t b)
+{
+    uint64_t s = a + b;
+    uint64_t t = s + ((s < a) ? EPS : 0);
+    // A second wrap needs both operands above p; fold it the same way.
+    return t + ((t < s) ? EPS : 0);
+}
+
+// a + b where b < p (or any b <= 2^64 - 2^32): a single wrap at most.
+__host__ __device__ __forceinline__ uint64_t gl_add_small(uint64_t a, uint64_t b)
+{
+    uint64_t s = a + b;
+    return s + ((s < b) ? EPS : 0);
+}
+
+// a - b for any a, b < 2^64.
+__host__ __device__ __forceinline__ uint64_t gl_sub(uint64_t a, uint64_t b)
+{
+    uint64_t d = a - b;
+    uint64_t t = d - ((a < b) ? EPS : 0);
+    return t - ((t > d) ? EPS : 0);
+}
+
+__host__ __device__ __forceinline__ uint64_t gl_neg(uint64_t a) { return gl_sub(0, a); }
+
+__host__ __device__ __forceinline__ uint64_t gl_double(uint64_t a) { return gl_add(a, a); }
+
+// Reduce the 128-bit value (r3:r2:r1:r0, 32-bit limbs) mod p:
+// x = lo64 + r2 * 2^64 + r3 * 2^96 = lo64 + r2 * eps - r3.
+__host__ __device__ __forceinline__ uint64_t gl_reduce128(uint64_t lo, uint64_t hi)
+{
+    const uint64_t r3 = hi >> 32;
+    const uint64_t r2 = hi & 0xFFFFFFFFull;
+    uint64_t t0 = lo - r3;
+    if (lo < r3) t0 -= EPS;  // borrow: t0 >= 2^64 - 2^32 + 1 > eps, no second wrap
+    const uint64_t t1 = (r2 << 32) - r2;  // r2 * eps < p
+    uint64_t r = t0 + t1;
+    if (r < t1) r += EPS;  // carry: result < t1 < p - eps, no second wrap
+    return r;
+}
+
+__host__ __device__ __forceinline__ uint64_t gl_mul(uint64_t a, uint64_t b)
+{
+#if defined(__HIP_DEVICE_COMPILE__) || defined(ZK_LIMB_MUL_ON_HOST)
+    const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
+    const uint32_t b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+    const uint64_t p00 = (uint64_t)a0 * b0;
+    const uint64_t p01 = (uint64_t)a0 * b1 + (p00 >> 32);
+    const uint64_t p10 = (uint64_t)a1 * b0 + (uint32_t)p01;
+    const uint64_t p11 = (uint64_t)a1 * b1 + (p01 >> 32) + (p10 >> 32);
+    const uint64_t lo = (p10 << 32) | (uint32_t)p00;
+    return gl_reduce128(lo, p11);
+#else
+    const unsigned __int128 x = (unsigned __int128)a * b;
+    return gl_reduce128((uint64_t)x, (uint64_t)(x >> 64));
+#endif
+}
+
+__host__ __device__ __forceinline__ uint64_t gl_sqr(uint64_t a)
+{
+#if defined(__HIP_DEVICE_COMPILE__) || defined(ZK_LIMB_MUL_ON_HOST)
+    const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
+    const uint64_t p00 = (uint64_t)a0 * a0;
+    const uint64_t c = (uint64_t)a0 * a1;  // cross term, counted twice
+    const uint64_t p01 = c + (p00 >> 32);
+    const uint64_t p10 = c + (uint32_t)p01;
+    const uint64_t p11 = (uint64_t)a1 * a1 + (p01 >> 32) + (p10 >> 32);
+    const uint64_t lo = (p10 << 32) | (uint32_t)p00;
+    return gl_reduce128(lo, p11);
+#else
+    return gl_mul(a, a);
+#endif
+}
+
+// x * 2^-k for 1 <= k <= 32, any x < 2^64:
+// x = q 2^k + r, r 2^-k = -r 2^(96-k) = -(m * eps) with m = r 2^(32-k) < 2^32,
+// and -(m * eps) = p - m 2^32 + m = (2^32 - 1 - m) 2^32 + (m + 1).
+template <int K>
+__host__ __device__ __forceinline__ uint64_t gl_mul_inv_pow2(uint64_t x)
+{
+    static_assert(K >= 1 && K <= 32, "shift range");
+    const uint64_t q = x >> K;
+    const uint64_t m = (K == 32) ? (x & 0xFFFFFFFFull) : ((x & ((1ull << K) - 1)) << (32 - K));
+    const uint64_t y = ((0xFFFFFFFFull - m) << 32) + (m + 1);
+    return gl_add_small(q, y) ;
+}
+
+__host__ __device__ __forceinline__ uint64_t gl_halve(uint64_t x)
+{
+    return (x >> 1) + ((x & 1) ? HALF : 0);
+}
+
+__host__ __device__ inline uint64_t gl_pow(uint64_t a, uint64_t e)
+{
+    uint64_t r = 1;
+    while (e) {
+        if (e & 1) r = gl_mul(r, a);
+        a = gl_mul(a, a);
+        e >>= 1;
+    }
+    return gl_canon(r);
+}
+
+__host__ __device__ inline uint64_t gl_inv(uint64_t a) { return gl_pow(a, P - 2); }
+
+// Lazy sum of up to 2^32 u64 terms: value = lo + hi * 2^64.
+struct Acc {
+    uint64_t lo;
+    uint32_t hi;
+};
+
+__host__ __device__ __forceinline__ Acc acc_of(uint64_t x) { return Acc{x, 0u}; }
+
+__host__ __device__ __forceinline__ Acc acc_add(Acc a, uint64_t x)
+{
+    const uint64_t s = a.lo + x;
+    return Acc{s, a.hi + (s < x ? 1u : 0u)};
+}
+
+__host__ __device__ __forceinline__ Acc acc_add(Acc a, Acc b)
+{
+    const uint64_t s = a.lo + b.lo;
+    return Acc{s, a.hi + b.hi + (s < b.lo ? 1u : 0u)};
+}
+
+// lo + hi * eps with hi * eps < p: one wrap at most.
+__host__ __device__ __forceinline__ uint64_t acc_reduce(Acc a)
+{
+    const uint64_t t = ((uint64_t)a.hi << 32) - (uint64_t)a.hi;
+    return gl_add_small(a.lo, t);
+}
+
+// Quadratic extension EF = F[x]/(x^2 - 7).
+struct Ef {
+    uint64_t c0, c1;
+};
+
+__host__ __device__ __forceinline__ Ef ef_add(Ef a, Ef b) { return Ef{gl_add(a.c0, b.c0), gl_add(a.c1, b.c1)}; }
+__host__ __device__ __forceinline__ Ef ef_sub(Ef a, Ef b) { return Ef{gl_sub(a.c0, b.c0), gl_sub(a.c1, b.c1)}; }
+
+__host__ __device__ __forceinline__ uint64_t gl_mul7(uint64_t x)
+{
+    const uint64_t x2 = gl_double(x), x4 = gl_double(x2);
+    return gl_add(gl_add(x4, x2), x);
+}
+
+__host__ __device__ __forceinline__ Ef ef_mul(Ef a, Ef b)
+{
+    const uint64_t c0 = gl_add(gl_mul(a.c0, b.c0), gl_mul7(gl_mul(a.c1, b.c1)));
+    const uint64_t c1 = gl_add(gl_mul(a.c0, b.c1), gl_mul(a.c1, b.c0));
+    return Ef{c0, c1};
+}
+
+__host__ __device__ __forceinline__ Ef ef_mul_base(Ef a, uint64_t b) { return Ef{gl_mul(a.c0, b), gl_mul(a.c1, b)}; }
+
+}  // namespace zk

@@ -1,0 +1,585 @@
+// Poseidon2 Merkle commitment on MI355X.
+//
+// Replaces crates/zkie-core/cuda/poseidon2_merkle.cu and the host schedule of
+// crates/zkie-core/src/pcs/merkle_cuda.rs:177-312. Design:
+//  * one row (leaf) or one parent (compression) per lane, so a wave of 64
+//    lanes runs 64 independent permutations; the reference kernel instead
+//    hashes 8 rows serially per thread (poseidon2_merkle.cu:187-196);
+//  * the upper tree levels, where a level has too few parents to fill the
+//    GPU, are reduced by one workgroup per subtree inside LDS (a level per
+//    barrier) instead of one kernel launch per level (merkle_cuda.rs:250-280);
+//  * the digest layers stay in HBM; openings gather rows and siblings on the
+//    device and copy only what was asked for.
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "poseidon2.hpp"
+#include "runtime.hpp"
+
+namespace zk {
+
+__constant__ P2Consts c_p2;
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+bool g_uploaded[kMaxDevices];
+bool g_diag_fast[kMaxDevices];
+std::mutex g_const_mu;
+
+// ---- host derivation of the constants (merkle_cuda.rs:54-85) -------------
+// rand 0.10 SmallRng = Xoshiro256++ seeded through SplitMix64; p3-goldilocks
+// samples a field element by rejecting u64 >= p.
+struct Xoshiro {
+    uint64_t s[4];
+    explicit Xoshiro(uint64_t seed)
+    {
+        uint64_t st = seed;
+        for (int i = 0; i < 4; i++) {
+            st += 0x9e3779b97f4a7c15ull;
+            uint64_t z = st;
+            z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+            z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+            s[i] = z ^ (z >> 31);
+        }
+    }
+    static uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+    uint64_t next()
+    {
+        const uint64_t res = rotl(s[0] + s[3], 23) + s[0];
+        const uint64_t t = s[1] << 17;
+        s[2] ^= s[0];
+        s[3] ^= s[1];
+        s[1] ^= s[2];
+        s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = rotl(s[3], 45);
+        return res;
+    }
+    uint64_t field()
+    {
+        for (;;) {
+            uint64_t x = next();
+            if (x < P) return x;
+        }
+    }
+};
+
+void derive_default(P2Consts& c)
+{
+    Xoshiro r(1);
+    for (int k = 0; k < 4; k++)
+        for (int i = 0; i < 16; i++) c.ext[k][i] = r.field();
+    for (int k = 4; k < 8; k++)
+        for (int i = 0; i < 16; i++) c.ext[k][i] = r.field();
+    for (int k = 0; k < 22; k++) c.internal[k] = r.field();
+    c.diag15 = INV_2_32;
+}
+
+int upload(const P2Consts& c)
+{
+    const int dev = current_device();
+    if (dev < 0 || dev >= kMaxDevices) return ZKIE_ERR_INVALID;
+    ZK_TRY(hipMemcpyToSymbol(HIP_SYMBOL(c_p2), &c, sizeof(P2Consts), 0, hipMemcpyHostToDevice));
+    g_uploaded[dev] = true;
+    g_diag_fast[dev] = gl_canon(c.diag15) == INV_2_32;
+    return ZKIE_OK;
+}
+
+// Upload the default constants on first use of a device; report whether
+// the 2^-32 diagonal fast path applies.
+int ensure_constants(bool* diag_fast)
+{
+    std::lock_guard<std::mutex> g(g_const_mu);
+    const int dev = current_device();
+    if (dev < 0 || dev >= kMaxDevices) return ZKIE_ERR_INVALID;
+    if (!g_uploaded[dev]) {
+        P2Consts c;
+        derive_default(c);
+        int rc = upload(c);
+        if (rc) return rc;
+    }
+    *diag_fast = g_diag_fast[dev];
+    return ZKIE_OK;
+}
+
+// ---- device helpers --------------------------------------------------------
+__device__ __forceinline__ void store_digest(uint64_t* dst, const uint64_t* st)
+{
+    ulonglong2* d = reinterpret_cast<ulonglong2*>(dst);
+#pragma unroll
+    for (int k = 0; k < 4; k++) d[k] = make_ulonglong2(gl_canon(st[2 * k]), gl_canon(st[2 * k + 1]));
+}
+
+__device__ __forceinline__ void load8(uint64_t* st, const uint64_t* src)
+{
+    const ulonglong2* s = reinterpret_cast<const ulonglong2*>(src);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const ulonglong2 v = s[k];
+        st[2 * k] = v.x;
+        st[2 * k + 1] = v.y;
+    }
+}
+
+// Sponge absorption of one row of W elements (W known at compile time when
+// W > 0, else the runtime width w): PaddingFreeSponge<Perm, 16, 8, 8>.
+template <int W, bool D15>
+__device__ __forceinline__ void hash_row(const uint64_t* __restrict__ row, uint64_t w, uint64_t* st)
+{
+#pragma unroll
+    for (int i = 0; i < 16; i++) st[i] = 0;
+    if (W > 0) {
+        constexpr int kFull = W / 8, kRem = W % 8;
+#pragma unroll 1
+        for (int b = 0; b < kFull; b++) {
+            if ((W % 2) == 0) {
+                load8(st, row + 8 * b);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) st[i] = row[8 * b + i];
+            }
+            p2_permute<D15>(st, c_p2);
+        }
+        if (kRem) {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (i < kRem) st[i] = row[8 * kFull + i];
+            p2_permute<D15>(st, c_p2);
+        }
+    } else {
+#pragma unroll 1
+        for (uint64_t pos = 0; pos < w; pos += 8) {
+            const uint64_t len = w - pos < 8 ? w - pos : 8;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if ((uint64_t)i < len) st[i] = row[pos + i];
+            p2_permute<D15>(st, c_p2);
+        }
+    }
+}
+
+// Leaf digests of rows [row0, row_end).
+template <int W, bool D15>
+__global__ __launch_bounds__(256) void leaf_kernel(const uint64_t* __restrict__ mat,
+                                                   uint64_t* __restrict__ digests, uint64_t row0,
+                                                   uint64_t row_end, uint64_t w)
+{
+    const uint64_t row = row0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= row_end) return;
+    uint64_t st[16];
+    hash_row<W, D15>(mat + row * (W > 0 ? (uint64_t)W : w), w, st);
+    store_digest(digests + row * 8, st);
+}
+
+// Parents [from, to) of `step` children each; slots [to, pad_to) get the
+// zero digest (merkle_tree.rs:393-396 default digest padding).
+template <bool D15>
+__global__ __launch_bounds__(256) void compress_kernel(const uint64_t* __restrict__ prev,
+                                                       uint64_t* __restrict__ next, uint64_t from,
+                                                       uint64_t to, uint64_t pad_to, uint32_t step)
+{
+    const uint64_t i = from + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= pad_to) return;
+    uint64_t st[16];
+    if (i >= to) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) st[k] = 0;
+        store_digest(next + i * 8, st);
+        return;
+    }
+    load8(st, prev + (uint64_t)step * i * 8);
+    if (step == 2) {
+        load8(st + 8, prev + ((uint64_t)step * i + 1) * 8);
+    } else {
+#pragma unroll
+        for (int k = 8; k < 16; k++) st[k] = 0;
+    }
+    p2_permute<D15>(st, c_p2);
+    store_digest(next + i * 8, st);
+}
+
+// One workgroup reduces 2^levels consecutive digests of a layer to one
+// digest, writing every intermediate layer: the top of the tree in LDS, one
+// level per barrier. Parent j of level t (t = 1..levels) of subtree g is
+// written to out_layers[t-1] + (g << (levels - t)) + j.
+struct SubtreeArgs {
+    const uint64_t* in;    // first layer (already computed), 2^levels * groups digests
+    uint64_t* out[24];     // output layer base pointers, level 1..levels
+    uint32_t levels;
+};
+
+template <bool D15>
+__global__ __launch_bounds__(256) void subtree_kernel(SubtreeArgs a)
+{
+    __shared__ uint64_t lds[256 * 8];  // up to 256 digests of the current level
+    const uint32_t g = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    uint32_t n = 1u << a.levels;       // digests at the current level (<= 512)
+    const uint64_t* src = a.in + ((uint64_t)g << a.levels) * 8;
+    // Level 1 reads its children straight from the input layer.
+    for (uint32_t t = 1; t <= a.levels; t++) {
+        const uint32_t parents = n >> 1;
+        uint64_t st[16];
+        const bool active = tid < parents;
+        if (active) {
+            if (t == 1) {
+                load8(st, src + (uint64_t)(2 * tid) * 8);
+                load8(st + 8, src + (uint64_t)(2 * tid + 1) * 8);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; k++) st[k] = lds[(2 * tid) * 8 + k];
+            }
+            p2_permute<D15>(st, c_p2);
+        }
+        __syncthreads();
+        if (active) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) lds[tid * 8 + k] = gl_canon(st[k]);
+            store_digest(a.out[t - 1] + (((uint64_t)g << (a.levels - t)) + tid) * 8, st);
+        }
+        __syncthreads();
+        n = parents;
+    }
+}
+
+// Gather `count` records of `len` u64 at record ids ids[k] from src (record
+// stride `stride` u64) into dst (contiguous).
+__global__ __launch_bounds__(256) void gather_kernel(const uint64_t* __restrict__ src,
+                                                     uint64_t stride, uint64_t len,
+                                                     const uint64_t* __restrict__ ids,
+                                                     uint64_t count, uint64_t* __restrict__ dst)
+{
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= count * len) return;
+    const uint64_t k = t / len, e = t % len;
+    dst[t] = src[ids[k] * stride + e];
+}
+
+unsigned grid_for(uint64_t n, unsigned block = 256) { return (unsigned)((n + block - 1) / block); }
+
+// Launch the leaf kernel for rows [r0, r1) with a width specialisation.
+int launch_leaves(const uint64_t* mat, uint64_t* dig, uint64_t r0, uint64_t r1, uint64_t w,
+                  bool fast, hipStream_t s)
+{
+    if (r1 <= r0) return ZKIE_OK;
+    const unsigned grid = grid_for(r1 - r0);
+    ProfMark m = prof_begin("p2_leaf", s);
+#define ZK_LEAF(WW)                                                                                   \
+    do {                                                                                              \
+        if (fast)                                                                                     \
+            leaf_kernel<WW, true><<<grid, 256, 0, s>>>(mat, dig, r0, r1, w);                          \
+        else                                                                                          \
+            leaf_kernel<WW, false><<<grid, 256, 0, s>>>(mat, dig, r0, r1, w);                         \
+    } while (0)
+    switch (w) {
+        case 1: ZK_LEAF(1); break;
+        case 8: ZK_LEAF(8); break;
+        case 16: ZK_LEAF(16); break;
+        case 32: ZK_LEAF(32); break;
+        case 128: ZK_LEAF(128); break;
+        default: ZK_LEAF(0); break;
+    }
+#undef ZK_LEAF
+    prof_end(m, s);
+    ZK_LAUNCHED();
+    return ZKIE_OK;
+}
+
+int launch_compress(const uint64_t* prev, uint64_t* next, uint64_t from, uint64_t to,
+                    uint64_t pad_to, uint32_t step, bool fast, hipStream_t s)
+{
+    if (pad_to <= from) return ZKIE_OK;
+    const unsigned grid = grid_for(pad_to - from);
+    ProfMark m = prof_begin("p2_compress", s);
+    if (fast)
+        compress_kernel<true><<<grid, 256, 0, s>>>(prev, next, from, to, pad_to, step);
+    else
+        compress_kernel<false><<<grid, 256, 0, s>>>(prev, next, from, to, pad_to, step);
+    prof_end(m, s);
+    ZK_LAUNCHED();
+    return ZKIE_OK;
+}
+
+std::vector<uint64_t> layer_lens(uint64_t h)
+{
+    auto padded = [](uint64_t raw) -> uint64_t {
+        if (raw <= 1) return raw;
+        return (raw + 1) / 2 * 2;
+    };
+    std::vector<uint64_t> lens;
+    uint64_t len = padded(h);
+    lens.push_back(len);
+    while (len > 1) {
+        len = padded(len / 2);
+        lens.push_back(len);
+    }
+    return lens;
+}
+
+// Build every layer above layer 0 (layer 0 already filled and padded).
+// Levels whose parent count is a power of two and small enough are reduced
+// by the LDS subtree kernel; the rest go one launch per level.
+int build_upper(uint64_t* d_layers, const std::vector<uint64_t>& lens, bool fast, hipStream_t s)
+{
+    std::vector<uint64_t> off(lens.size());
+    uint64_t acc = 0;
+    for (size_t i = 0; i < lens.size(); i++) {
+        off[i] = acc;
+        acc += lens[i] * 8;
+    }
+    size_t i = 0;
+    const size_t top = lens.size() - 1;
+    while (i < top) {
+        const uint64_t len = lens[i];
+        // Subtree path: a power-of-two layer of at most 2^kSub digests
+        // reduces to the root in one launch (all levels above are exact
+        // halvings, no padding).
+        constexpr uint32_t kSub = 9;  // 512 digests -> 256 parents in LDS
+        if ((len & (len - 1)) == 0 && len <= (1ull << kSub) && len >= 2) {
+            SubtreeArgs a;
+            a.in = d_layers + off[i];
+            uint32_t levels = 0;
+            while ((1ull << levels) < len) levels++;
+            a.levels = levels;
+            for (uint32_t t = 1; t <= levels; t++) a.out[t - 1] = d_layers + off[i + t];
+            ProfMark m = prof_begin("p2_subtree", s);
+            if (fast)
+                subtree_kernel<true><<<1, 256, 0, s>>>(a);
+            else
+                subtree_kernel<false><<<1, 256, 0, s>>>(a);
+            prof_end(m, s);
+            ZK_LAUNCHED();
+            return ZKIE_OK;
+        }
+        const uint64_t raw = len / 2;
+        int rc = launch_compress(d_layers + off[i], d_layers + off[i + 1], 0, raw, lens[i + 1], 2,
+                                 fast, s);
+        if (rc) return rc;
+        i++;
+    }
+    return ZKIE_OK;
+}
+
+}  // namespace
+
+// Exposed to the other translation units of the library.
+int merkle_commit_device(const uint64_t* d_mat, uint64_t h, uint64_t w, uint64_t* d_layers,
+                         hipStream_t s)
+{
+    bool fast = false;
+    int rc = ensure_constants(&fast);
+    if (rc) return rc;
+    const std::vector<uint64_t> lens = layer_lens(h);
+    rc = launch_leaves(d_mat, d_layers, 0, h, w, fast, s);
+    if (rc) return rc;
+    if (lens[0] > h) {
+        rc = launch_compress(nullptr, d_layers, h, h, lens[0], 2, fast, s);  // zero digests only
+        if (rc) return rc;
+    }
+    if (lens.size() == 1) return ZKIE_OK;
+    return build_upper(d_layers, lens, fast, s);
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" {
+
+int zkie_p2_default_constants(uint64_t rc_init[64], uint64_t rc_final[64], uint64_t rc_internal[22],
+                              uint64_t* diag15)
+{
+    if (!rc_init || !rc_final || !rc_internal || !diag15) return ZKIE_ERR_INVALID;
+    P2Consts c;
+    derive_default(c);
+    for (int k = 0; k < 4; k++)
+        for (int i = 0; i < 16; i++) {
+            rc_init[16 * k + i] = c.ext[k][i];
+            rc_final[16 * k + i] = c.ext[4 + k][i];
+        }
+    for (int k = 0; k < 22; k++) rc_internal[k] = c.internal[k];
+    *diag15 = c.diag15;
+    return ZKIE_OK;
+}
+
+int zkie_p2_upload_constants(const uint64_t* rc_init, const uint64_t* rc_final,
+                             const uint64_t* rc_internal, uint64_t diag15)
+{
+    if (!rc_init || !rc_final || !rc_internal) return ZKIE_ERR_INVALID;
+    P2Consts c;
+    for (int k = 0; k < 4; k++)
+        for (int i = 0; i < 16; i++) {
+            c.ext[k][i] = gl_canon(rc_init[16 * k + i]);
+            c.ext[4 + k][i] = gl_canon(rc_final[16 * k + i]);
+        }
+    for (int k = 0; k < 22; k++) c.internal[k] = gl_canon(rc_internal[k]);
+    c.diag15 = gl_canon(diag15);
+    std::lock_guard<std::mutex> g(g_const_mu);
+    return upload(c);
+}
+
+int zkie_p2_leaf_batch(const uint64_t* d_mat, uint64_t* d_digests, uint32_t h, uint32_t w)
+{
+    bool fast = false;
+    int rc = ensure_constants(&fast);
+    if (rc) return rc;
+    return launch_leaves(d_mat, d_digests, 0, (uint64_t)(h / 8) * 8, w, fast, 0);
+}
+
+int zkie_p2_leaf_scalar(const uint64_t* d_mat, uint64_t* d_digests, uint32_t start_row, uint32_t h,
+                        uint32_t w)
+{
+    bool fast = false;
+    int rc = ensure_constants(&fast);
+    if (rc) return rc;
+    return launch_leaves(d_mat, d_digests, start_row, h, w, fast, 0);
+}
+
+int zkie_p2_compress_batch(const uint64_t* d_prev, uint64_t* d_next, uint32_t next_len, uint32_t step)
+{
+    if (step != 1 && step != 2) return ZKIE_ERR_INVALID;
+    bool fast = false;
+    int rc = ensure_constants(&fast);
+    if (rc) return rc;
+    const uint64_t end = (uint64_t)(next_len / 8) * 8;
+    return launch_compress(d_prev, d_next, 0, end, end, step, fast, 0);
+}
+
+int zkie_p2_compress_scalar(const uint64_t* d_prev, uint64_t* d_next, uint32_t from, uint32_t to,
+                            uint32_t step)
+{
+    if (step != 1 && step != 2) return ZKIE_ERR_INVALID;
+    bool fast = false;
+    int rc = ensure_constants(&fast);
+    if (rc) return rc;
+    return launch_compress(d_prev, d_next, from, to, to, step, fast, 0);
+}
+
+int zkie_merkle_layout(uint64_t h, uint32_t* num_layers, uint64_t* layer_lens_out)
+{
+    if (h == 0 || !num_layers) return ZKIE_ERR_INVALID;
+    const std::vector<uint64_t> lens = layer_lens(h);
+    *num_layers = (uint32_t)lens.size();
+    if (layer_lens_out)
+        for (size_t i = 0; i < lens.size(); i++) layer_lens_out[i] = lens[i];
+    return ZKIE_OK;
+}
+
+int zkie_merkle_commit(const uint64_t* d_mat, uint64_t h, uint64_t w, uint64_t* d_layers,
+                       uint64_t* root, void* stream)
+{
+    if (h == 0 || !d_layers || (w > 0 && !d_mat)) return ZKIE_ERR_INVALID;
+    hipStream_t s = as_stream(stream);
+    int rc = merkle_commit_device(d_mat, h, w, d_layers, s);
+    if (rc) return rc;
+    if (root) {
+        const std::vector<uint64_t> lens = layer_lens(h);
+        uint64_t off = 0;
+        for (size_t i = 0; i + 1 < lens.size(); i++) off += lens[i] * 8;
+        ZK_TRY(hipMemcpyAsync(root, d_layers + off, 64, hipMemcpyDeviceToHost, s));
+        ZK_TRY(hipStreamSynchronize(s));
+    }
+    return ZKIE_OK;
+}
+
+namespace {
+
+// Copy `ids.size()` records of `len` u64 from src into host memory `out`.
+int gather_to_host(const uint64_t* d_src, uint64_t stride, uint64_t len,
+                   const std::vector<uint64_t>& ids, uint64_t* out, hipStream_t s)
+{
+    if (ids.empty() || len == 0) return ZKIE_OK;
+    const uint64_t count = ids.size();
+    const size_t bytes_ids = count * 8, bytes_out = count * len * 8;
+    uint8_t* ws = (uint8_t*)workspace(WS_MISC, bytes_ids + bytes_out);
+    if (!ws) return ZKIE_ERR_ALLOC;
+    uint64_t* d_ids = (uint64_t*)ws;
+    uint64_t* d_out = (uint64_t*)(ws + bytes_ids);
+    ZK_TRY(hipMemcpyAsync(d_ids, ids.data(), bytes_ids, hipMemcpyHostToDevice, s));
+    gather_kernel<<<grid_for(count * len), 256, 0, s>>>(d_src, stride, len, d_ids, count, d_out);
+    ZK_LAUNCHED();
+    ZK_TRY(hipMemcpyAsync(out, d_out, bytes_out, hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    return ZKIE_OK;
+}
+
+}  // namespace
+
+int zkie_merkle_open_batch(const uint64_t* d_mat, uint64_t h, uint64_t w, const uint64_t* d_layers,
+                           const uint64_t* indices, uint64_t n, uint64_t* rows_out,
+                           uint64_t* siblings_out, void* stream)
+{
+    if (h == 0 || !d_layers || (n && !indices)) return ZKIE_ERR_INVALID;
+    for (uint64_t k = 0; k < n; k++)
+        if (indices[k] >= h) return ZKIE_ERR_INVALID;
+    hipStream_t s = as_stream(stream);
+    const std::vector<uint64_t> lens = layer_lens(h);
+    if (rows_out && w > 0) {
+        std::vector<uint64_t> rows(indices, indices + n);
+        int rc = gather_to_host(d_mat, w, w, rows, rows_out, s);
+        if (rc) return rc;
+    }
+    if (siblings_out && lens.size() > 1) {
+        std::vector<uint64_t> ids;
+        ids.reserve(n * (lens.size() - 1));
+        for (uint64_t k = 0; k < n; k++) {
+            uint64_t idx = indices[k], base = 0;
+            for (size_t l = 0; l + 1 < lens.size(); l++) {
+                ids.push_back(base + (idx ^ 1));
+                base += lens[l];
+                idx >>= 1;
+            }
+        }
+        int rc = gather_to_host(d_layers, 8, 8, ids, siblings_out, s);
+        if (rc) return rc;
+    }
+    return ZKIE_OK;
+}
+
+int zkie_merkle_open_pruned(const uint64_t* d_mat, uint64_t h, uint64_t w, const uint64_t* d_layers,
+                            const uint64_t* indices, uint64_t n, uint64_t* rows_out,
+                            uint64_t* pruned_out, uint64_t cap, uint64_t* count, void* stream)
+{
+    if (h == 0 || !d_layers || !count || (n && !indices)) return ZKIE_ERR_INVALID;
+    for (uint64_t k = 0; k < n; k++)
+        if (indices[k] >= h) return ZKIE_ERR_INVALID;
+    hipStream_t s = as_stream(stream);
+    const std::vector<uint64_t> lens = layer_lens(h);
+    if (rows_out && w > 0) {
+        std::vector<uint64_t> rows(indices, indices + n);
+        int rc = gather_to_host(d_mat, w, w, rows, rows_out, s);
+        if (rc) return rc;
+    }
+    // walk_frontier (pruning.rs:130-170), arity 2 at every level.
+    std::vector<uint64_t> nodes(indices, indices + n);
+    std::sort(nodes.begin(), nodes.end());
+    nodes.erase(std::unique(nodes.begin(), nodes.end()), nodes.end());
+    std::vector<uint64_t> ids;
+    uint64_t base = 0;
+    for (size_t l = 0; l + 1 < lens.size() && !nodes.empty(); l++) {
+        std::vector<uint64_t> parents;
+        size_t i = 0;
+        while (i < nodes.size()) {
+            const uint64_t group = nodes[i] / 2, start = group * 2;
+            size_t member = i;
+            for (uint64_t k = 0; k < 2; k++) {
+                if (member < nodes.size() && nodes[member] == start + k)
+                    member++;
+                else
+                    ids.push_back(base + start + k);
+            }
+            parents.push_back(group);
+            i = member;
+        }
+        nodes.swap(parents);
+        base += lens[l];
+    }
+    *count = ids.size();
+    if (ids.size() > cap) return ZKIE_ERR_INVALID;
+    if (!pruned_out) return ids.empty() ? ZKIE_OK : ZKIE_ERR_INVALID;
+    return gather_to_host(d_layers, 8, 8, ids, pruned_out, s);
+}
+
+}  // extern "C"

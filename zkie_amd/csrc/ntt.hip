@@ -1,0 +1,198 @@
+// Batched Goldilocks NTT on MI355X.
+//
+// Replaces crates/zkie-core/cuda/goldilocks_ntt.cu (lg_h full-HBM radix-2
+// passes plus a scattered gather and scatter, capped at 2^18 rows by
+// dft_cuda.rs:96) with a four-step decomposition:
+//   n = 2^L is split into P passes of s_p bits (s_p <= 9). Pass p treats the
+//   array as independent blocks of N = 2^B rows (B = L - s_0 - ... - s_{p-1}),
+//   splits N = N1 * N2 with N1 = 2^(s_p) and computes, for every j2 < N2,
+//       Y[i1][j2] = w_N^(i1 j2) * sum_j1 x[j1 N2 + j2] w_N1^(i1 j1)
+//   into position i1 N2 + j2 of the block (in place), with the N1-point DFT
+//   done as radix-2 decimation-in-frequency stages inside LDS. The last pass
+//   (N2 = 1) writes each result straight to its natural row.
+// A workgroup owns an N1 x V tile, V = C columns x J consecutive j2 values,
+// chosen so that every global access of one point is a contiguous run of
+// C*J*8 = 128 bytes (16 columns of a row, or 16 consecutive rows of a
+// single column), i.e. whole cache lines.
+// The first pass of an LDE reads only the h non-zero input rows; the zero
+// rows of the padded matrix are never materialised or read.
+#include <mutex>
+#include <vector>
+
+#include "ntt_plan.hpp"
+#include "runtime.hpp"
+
+namespace zk {
+namespace {
+
+constexpr int kMaxDevices = 64;
+uint64_t* g_tables[kMaxDevices];
+std::mutex g_tab_mu;
+
+int ensure_tables(const uint64_t** out)
+{
+    std::lock_guard<std::mutex> g(g_tab_mu);
+    const int dev = current_device();
+    if (dev < 0 || dev >= kMaxDevices) return ZKIE_ERR_INVALID;
+    if (!g_tables[dev]) {
+        const std::vector<uint64_t> h = build_twiddle_tables();
+        void* d = nullptr;
+        ZK_TRY(hipMalloc(&d, h.size() * 8));
+        ZK_TRY(hipMemcpy(d, h.data(), h.size() * 8, hipMemcpyHostToDevice));
+        g_tables[dev] = (uint64_t*)d;
+    }
+    *out = g_tables[dev];
+    return ZKIE_OK;
+}
+
+__global__ __launch_bounds__(256) void ntt_pass_kernel(PassArgs a)
+{
+    extern __shared__ uint64_t lds[];
+    const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
+    const PassTile t = pass_tile(a, bid);
+    pass_load(a, t, threadIdx.x, blockDim.x, lds);
+    __syncthreads();
+    for (int lm = (int)a.s - 1; lm >= 0; lm--) {
+        pass_stage(a, t, lm, threadIdx.x, blockDim.x, lds);
+        __syncthreads();
+    }
+    pass_store(a, t, threadIdx.x, blockDim.x, lds);
+}
+
+// Multiply row j of an h x w matrix by shift^j, shift^j = lo[j & 0xFFFF] * hi[j >> 16].
+__global__ __launch_bounds__(256) void coset_scale_kernel(const uint64_t* __restrict__ in,
+                                                          uint64_t* __restrict__ out, uint64_t h,
+                                                          uint64_t w, const uint64_t* __restrict__ lo,
+                                                          const uint64_t* __restrict__ hi)
+{
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= h * w) return;
+    const uint64_t j = t / w;
+    const uint64_t sj = gl_mul(lo[j & 0xFFFF], hi[j >> 16]);
+    out[t] = gl_mul(in[t], sj);
+}
+
+// Run all passes (see pass_args for the buffer roles).
+int run_passes(const Plan& p, uint64_t w, const uint64_t* in, uint64_t in_rows, uint64_t* tmp,
+               uint64_t* out, bool inverse, hipStream_t s)
+{
+    const uint64_t* tables = nullptr;
+    int rc = ensure_tables(&tables);
+    if (rc) return rc;
+    uint32_t B = p.L;
+    for (uint32_t i = 0; i < p.np; i++) {
+        const PassArgs a = pass_args(p, i, B, w, in, in_rows, tmp, out, tables, inverse);
+        const uint64_t blocks = pass_blocks(a);
+        dim3 grid;
+        if (blocks <= 0x7FFFFFFFull) {
+            grid = dim3((unsigned)blocks, 1, 1);
+        } else {
+            const uint64_t gx = 65536;
+            if ((blocks % gx) != 0) return ZKIE_ERR_INVALID;
+            grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
+        }
+        ProfMark m = prof_begin(a.last ? "ntt_pass_last" : "ntt_pass", s);
+        ntt_pass_kernel<<<grid, 256, pass_lds_bytes(a), s>>>(a);
+        prof_end(m, s);
+        ZK_LAUNCHED();
+        B -= a.s;
+    }
+    return ZKIE_OK;
+}
+
+int dft_inplace(uint64_t* d_mat, uint64_t* d_tmp, uint32_t lg, uint64_t w, bool inverse, hipStream_t s)
+{
+    if (lg > 32 || (w > 0 && !d_mat)) return ZKIE_ERR_INVALID;
+    if (lg == 0 || w == 0) return ZKIE_OK;
+    const Plan p = make_plan(lg, w);
+    const uint64_t n = 1ull << lg;
+    if (p.np == 1) return run_passes(p, w, d_mat, n, nullptr, d_mat, inverse, s);
+    if (!d_tmp) {
+        d_tmp = (uint64_t*)workspace(WS_NTT, n * w * 8);
+        if (!d_tmp) return ZKIE_ERR_ALLOC;
+    }
+    return run_passes(p, w, d_mat, n, d_tmp, d_mat, inverse, s);
+}
+
+}  // namespace
+
+// Exposed to the other translation units of the library.
+int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+               uint64_t* d_out, hipStream_t s)
+{
+    if (h == 0 || (h & (h - 1)) != 0 || !d_in || !d_out) return ZKIE_ERR_INVALID;
+    uint32_t lgh = 0;
+    while ((1ull << lgh) < h) lgh++;
+    const uint32_t L = lgh + log_blowup;
+    if (L > 32) return ZKIE_ERR_INVALID;
+    if (w == 0) return ZKIE_OK;
+    const uint64_t n = 1ull << L;
+    const uint64_t* src = d_in;
+    shift = gl_canon(shift);
+    if (shift != 1) {
+        // coset: x_j <- x_j shift^j, staged in the head of d_out.
+        std::vector<uint64_t> tab(2 * kBigLen);
+        uint64_t x = 1;
+        for (uint64_t k = 0; k < kBigLen; k++) {
+            tab[k] = x;
+            x = gl_canon(gl_mul(x, shift));
+        }
+        const uint64_t step = x;
+        x = 1;
+        for (uint64_t k = 0; k < kBigLen; k++) {
+            tab[kBigLen + k] = x;
+            x = gl_canon(gl_mul(x, step));
+        }
+        uint64_t* d_tab = (uint64_t*)workspace(WS_MISC, tab.size() * 8);
+        if (!d_tab) return ZKIE_ERR_ALLOC;
+        ZK_TRY(hipMemcpyAsync(d_tab, tab.data(), tab.size() * 8, hipMemcpyHostToDevice, s));
+        const uint64_t total = h * w;
+        coset_scale_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(d_in, d_out, h, w, d_tab,
+                                                                          d_tab + kBigLen);
+        ZK_LAUNCHED();
+        ZK_TRY(hipStreamSynchronize(s));  // the table buffer is reused by later calls
+        src = d_out;
+    }
+    const Plan p = make_plan(L, w);
+    if (p.np == 1) {
+        if (src == d_out) {
+            // in place, single pass: rows >= h are treated as zero
+            return run_passes(p, w, d_out, h, nullptr, d_out, false, s);
+        }
+        return run_passes(p, w, src, h, nullptr, d_out, false, s);
+    }
+    uint64_t* tmp = (uint64_t*)workspace(WS_NTT, n * w * 8);
+    if (!tmp) return ZKIE_ERR_ALLOC;
+    return run_passes(p, w, src, h, tmp, d_out, false, s);
+}
+
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" {
+
+int zkie_ntt_forward_goldilocks(uint64_t* d_mat, uint64_t* d_temp, uint32_t lg_h, uint64_t w,
+                                const uint64_t* d_tw)
+{
+    (void)d_tw;  // twiddles are generated internally (identical values)
+    return dft_inplace(d_mat, d_temp, lg_h, w, false, 0);
+}
+
+int zkie_dft_batch(uint64_t* d_mat, uint32_t lg_h, uint64_t w, void* stream)
+{
+    return dft_inplace(d_mat, nullptr, lg_h, w, false, as_stream(stream));
+}
+
+int zkie_idft_batch(uint64_t* d_mat, uint32_t lg_h, uint64_t w, void* stream)
+{
+    return dft_inplace(d_mat, nullptr, lg_h, w, true, as_stream(stream));
+}
+
+int zkie_lde_batch(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+                   uint64_t* d_out, void* stream)
+{
+    return lde_device(d_in, h, w, log_blowup, shift, d_out, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,112 @@
+// Host-side NTT planning and twiddle tables, shared by the library and the
+// CPU emulator of the device passes.
+#pragma once
+
+#include <vector>
+
+#include "ntt_pass.hpp"
+
+namespace zk {
+
+constexpr uint32_t kMaxPassBits = 9;
+constexpr uint32_t kSmallLg = 13;                 // small tables: w_{2^lg}, lg <= 13
+constexpr uint64_t kSmallLen = 1ull << kSmallLg;  // one table, offsets 2^(lg-1) - 1
+constexpr uint64_t kBigLen = 1ull << 16;          // two-level table of w_{2^32}
+constexpr uint64_t kTableLen = 2 * kSmallLen + 4 * kBigLen;
+
+// Table layout: [small_fwd | small_inv | lo_fwd | hi_fwd | lo_inv | hi_inv].
+inline const uint64_t* tab_small(const uint64_t* base, bool inv) { return base + (inv ? kSmallLen : 0); }
+inline const uint64_t* tab_lo(const uint64_t* base, bool inv) { return base + 2 * kSmallLen + (inv ? 2 * kBigLen : 0); }
+inline const uint64_t* tab_hi(const uint64_t* base, bool inv) { return tab_lo(base, inv) + kBigLen; }
+
+// TWO_ADIC_GENERATORS[k] = 7^((p-1)/2^k), the table dft_cuda.rs:49 reads.
+inline uint64_t two_adic_generator(uint32_t k) { return gl_pow(7, (P - 1) >> k); }
+
+inline std::vector<uint64_t> build_twiddle_tables()
+{
+    std::vector<uint64_t> h(kTableLen, 0);
+    for (int inv = 0; inv < 2; inv++) {
+        uint64_t* sm = h.data() + (inv ? kSmallLen : 0);
+        for (uint32_t lg = 1; lg <= kSmallLg; lg++) {
+            uint64_t root = two_adic_generator(lg);
+            if (inv) root = gl_inv(root);
+            const uint64_t off = (1ull << (lg - 1)) - 1;
+            uint64_t x = 1;
+            for (uint64_t k = 0; k < (1ull << (lg - 1)); k++) {
+                sm[off + k] = x;
+                x = gl_canon(gl_mul(x, root));
+            }
+        }
+        uint64_t g32 = two_adic_generator(32);
+        if (inv) g32 = gl_inv(g32);
+        uint64_t* lo = h.data() + 2 * kSmallLen + (inv ? 2 * kBigLen : 0);
+        uint64_t* hi = lo + kBigLen;
+        uint64_t x = 1;
+        for (uint64_t k = 0; k < kBigLen; k++) {
+            lo[k] = x;
+            x = gl_canon(gl_mul(x, g32));
+        }
+        const uint64_t step = x;  // g32^(2^16)
+        x = 1;
+        for (uint64_t k = 0; k < kBigLen; k++) {
+            hi[k] = x;
+            x = gl_canon(gl_mul(x, step));
+        }
+    }
+    return h;
+}
+
+struct Plan {
+    uint32_t L = 0, np = 0, logC = 0;
+    uint32_t sb[8] = {0};
+};
+
+inline Plan make_plan(uint32_t L, uint64_t w)
+{
+    Plan p;
+    p.L = L;
+    uint32_t logC = 0;
+    while (logC < 4 && (w % (2ull << logC)) == 0) logC++;
+    p.logC = logC;
+    p.np = L == 0 ? 0 : (L + kMaxPassBits - 1) / kMaxPassBits;
+    for (uint32_t i = 0; i < p.np; i++) p.sb[i] = L / p.np + (i < L % p.np ? 1 : 0);
+    return p;
+}
+
+// Arguments of pass i. Passes 0..np-2 read `in` (pass 0) or `tmp` and write
+// `tmp` in place; the last pass reads `tmp` (or `in` when np == 1) and writes
+// `out` in natural order. B is the block log-size entering pass i.
+inline PassArgs pass_args(const Plan& p, uint32_t i, uint32_t B, uint64_t w, const uint64_t* in,
+                          uint64_t in_rows, uint64_t* tmp, uint64_t* out, const uint64_t* tables,
+                          bool inverse)
+{
+    PassArgs a;
+    const uint64_t n = 1ull << p.L;
+    const bool last = (i + 1 == p.np);
+    a.in = i == 0 ? in : tmp;
+    a.out = last ? out : tmp;
+    a.in_rows = i == 0 ? in_rows : n;
+    a.w = w;
+    a.scale = last && inverse ? gl_inv(n % P) : 1;
+    a.tws = tab_small(tables, inverse);
+    a.twlo = tab_lo(tables, inverse);
+    a.twhi = tab_hi(tables, inverse);
+    a.in_len = (i == 0 ? in_rows : n) * w;
+    a.out_len = n * w;
+    a.L = p.L;
+    a.B = B;
+    a.s = p.sb[i];
+    a.logC = p.logC;
+    const uint32_t logN2 = B - a.s;
+    uint32_t logJ = 4 - p.logC;
+    if (logJ > logN2) logJ = logN2;
+    a.logJ = logJ;
+    a.last = last ? 1 : 0;
+    a.np = p.np;
+    for (int k = 0; k < 8; k++) a.sb[k] = p.sb[k];
+    return a;
+}
+
+inline size_t pass_lds_bytes(const PassArgs& a) { return ((size_t)1 << (a.s + a.logC + a.logJ)) * 8; }
+
+}  // namespace zk

@@ -1,0 +1,130 @@
+// Poseidon2-Goldilocks-16 on CDNA4: one permutation per lane, state in 16
+// u64 registers. Restates poseidon2_merkle.cu:37-155 (the reference device
+// permutation that mirrors p3-poseidon2 / p3-goldilocks 0.7.0):
+//   initial mds_light16, 4 external rounds (rc, x^7 on all lanes,
+//   mds_light16), 22 internal rounds (rc and x^7 on lane 0, then
+//   st_i = sum + V_i st_i), 4 external rounds.
+// V = [-2, 1, 2, 1/2, 3, 4, -1/2, -3, -4, 1/2^3, 1/2^4, 1/2^5, -1/2^3,
+//      -1/2^4, -1/2^5, diag15] (poseidon2_merkle.cu:111-142).
+//
+// MI355X choices:
+//  * round constants sit in __constant__ memory indexed by wave-uniform
+//    loop counters, so the compiler reads them with scalar loads into SGPRs
+//    and every VALU op takes them as a scalar operand;
+//  * the linear layers accumulate into a lazy 96-bit sum (Acc) and reduce
+//    once per output, instead of reducing after every addition, and the next
+//    round's constants are folded into that same reduction;
+//  * 1/2^k multiplies are shift/add sequences (gl_mul_inv_pow2), and the
+//    2^-32 entry uses the same closed form when diag15 has that value;
+//  * round loops stay rolled (one copy of the external round body) to keep
+//    the code inside the instruction cache.
+#pragma once
+
+#include "gl64.hpp"
+
+namespace zk {
+
+struct P2Consts {
+    uint64_t ext[8][16];  // [0..4) initial, [4..8) terminal external rounds
+    uint64_t internal[22];
+    uint64_t diag15;
+};
+
+__host__ __device__ __forceinline__ uint64_t sbox7(uint64_t x)
+{
+    const uint64_t x2 = gl_sqr(x);
+    const uint64_t x3 = gl_mul(x2, x);
+    const uint64_t x4 = gl_sqr(x2);
+    return gl_mul(x3, x4);
+}
+
+// mat4 = [2 3 1 1; 1 2 3 1; 1 1 2 3; 3 1 1 2] on lazy sums
+// (addition chain of poseidon2_merkle.cu:63-76).
+__host__ __device__ __forceinline__ void mat4_lazy(const uint64_t* x, Acc* y)
+{
+    const Acc t01 = acc_add(acc_of(x[0]), x[1]);
+    const Acc t23 = acc_add(acc_of(x[2]), x[3]);
+    const Acc t0123 = acc_add(t01, t23);
+    const Acc t01123 = acc_add(t0123, x[1]);
+    const Acc t01233 = acc_add(t0123, x[3]);
+    y[3] = acc_add(acc_add(t01233, x[0]), x[0]);  // 3x0 + x1 + x2 + 2x3
+    y[1] = acc_add(acc_add(t01123, x[2]), x[2]);  // x0 + 2x1 + 3x2 + x3
+    y[0] = acc_add(t01123, t01);                  // 2x0 + 3x1 + x2 + x3
+    y[2] = acc_add(t01233, t23);                  // x0 + x1 + 2x2 + 3x3
+}
+
+// st <- mds_light16(st) (+ rc if given), each output reduced once.
+template <bool ADD_RC>
+__host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_t* rc)
+{
+    Acc y[16];
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) mat4_lazy(st + j, y + j);
+    Acc sums[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) sums[k] = acc_add(acc_add(y[k], y[4 + k]), acc_add(y[8 + k], y[12 + k]));
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        Acc t = acc_add(y[i], sums[i & 3]);
+        if (ADD_RC) t = acc_add(t, rc[i]);
+        st[i] = acc_reduce(t);
+    }
+}
+
+template <bool DIAG15_IS_INV_2_32>
+__host__ __device__ __forceinline__ void internal_linear(uint64_t* st, uint64_t diag15)
+{
+    Acc s = acc_of(st[0]);
+#pragma unroll
+    for (int i = 1; i < 16; i++) s = acc_add(s, st[i]);
+    const uint64_t sum = acc_reduce(s);
+    const uint64_t x0 = st[0];
+    st[0] = gl_sub(sum, gl_double(x0));                       // -2
+    st[1] = gl_add(sum, st[1]);                               // 1
+    st[2] = gl_add(sum, gl_double(st[2]));                    // 2
+    st[3] = gl_add(sum, gl_halve(st[3]));                     // 1/2
+    st[4] = gl_add(sum, gl_add(gl_double(st[4]), st[4]));     // 3
+    st[5] = gl_add(sum, gl_double(gl_double(st[5])));         // 4
+    st[6] = gl_sub(sum, gl_halve(st[6]));                     // -1/2
+    st[7] = gl_sub(sum, gl_add(gl_double(st[7]), st[7]));     // -3
+    st[8] = gl_sub(sum, gl_double(gl_double(st[8])));         // -4
+    st[9] = gl_add(sum, gl_mul_inv_pow2<3>(st[9]));           // 1/2^3
+    st[10] = gl_add(sum, gl_mul_inv_pow2<4>(st[10]));         // 1/2^4
+    st[11] = gl_add(sum, gl_mul_inv_pow2<5>(st[11]));         // 1/2^5
+    st[12] = gl_sub(sum, gl_mul_inv_pow2<3>(st[12]));         // -1/2^3
+    st[13] = gl_sub(sum, gl_mul_inv_pow2<4>(st[13]));         // -1/2^4
+    st[14] = gl_sub(sum, gl_mul_inv_pow2<5>(st[14]));         // -1/2^5
+    if (DIAG15_IS_INV_2_32)
+        st[15] = gl_add(sum, gl_mul_inv_pow2<32>(st[15]));
+    else
+        st[15] = gl_add(sum, gl_mul(st[15], diag15));
+}
+
+template <bool DIAG15_IS_INV_2_32>
+__host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts& C)
+{
+    // Initial linear layer fused with the first round's constants.
+    mds_light16<true>(st, C.ext[0]);
+#pragma unroll 1
+    for (int r = 0; r < 8; r++) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) st[i] = sbox7(st[i]);
+        if (r == 3) {
+            mds_light16<false>(st, nullptr);
+#pragma unroll 1
+            for (int k = 0; k < 22; k++) {
+                st[0] = sbox7(gl_add_small(st[0], C.internal[k]));
+                internal_linear<DIAG15_IS_INV_2_32>(st, C.diag15);
+            }
+            // Constants of the first terminal round (st += rc) before its S-box.
+#pragma unroll
+            for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
+        } else if (r == 7) {
+            mds_light16<false>(st, nullptr);
+        } else {
+            mds_light16<true>(st, C.ext[r + 1]);
+        }
+    }
+}
+
+}  // namespace zk

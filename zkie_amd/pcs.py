@@ -1,0 +1,161 @@
+"""Python view of the per-stage dispatch seam, over the HIP C ABI.
+
+Mirrors the engines of the reference's WHIR wrapper:
+  * HipDft            <- CudaDft (crates/zkie-core/src/pcs/dft_cuda.rs:124-222),
+                         TwoAdicSubgroupDft::dft_batch on row-major matrices;
+  * HipMerkleTreeMmcs <- CudaMerkleTreeMmcs (merkle_cuda.rs:133-393),
+                         Mmcs::{commit, open_batch, open_multi_batch};
+  * HipMerkleTree     <- the MerkleTree prover data (p3-merkle-tree
+                         merkle_tree.rs:32-70), kept device-resident;
+  * fold_rows         <- the WHIR row fold (p3-whir prover/mod.rs:257-290).
+Unlike the reference there is no CPU fallback: every failure raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _native as N
+from ._native import DeviceBuffer, check
+
+
+def _as_matrix(mat) -> np.ndarray:
+    m = np.ascontiguousarray(np.asarray(mat, dtype=np.uint64))
+    if m.ndim == 1:
+        m = m.reshape(-1, 1)
+    return m
+
+
+class HipDft:
+    """TwoAdicSubgroupDft<Goldilocks> on the GPU (dft_cuda.rs:161-222)."""
+
+    def dft_batch(self, mat) -> np.ndarray:
+        m = _as_matrix(mat)
+        h, w = m.shape
+        if h <= 1:
+            return m.copy()
+        lg = h.bit_length() - 1
+        if 1 << lg != h:
+            raise ValueError("height must be a power of two")
+        d = DeviceBuffer.from_array(m)
+        check(N.load().zkie_dft_batch(d.addr, lg, w, None), "zkie_dft_batch")
+        return d.download().reshape(h, w)
+
+    def idft_batch(self, mat) -> np.ndarray:
+        m = _as_matrix(mat)
+        h, w = m.shape
+        lg = h.bit_length() - 1
+        d = DeviceBuffer.from_array(m)
+        check(N.load().zkie_idft_batch(d.addr, lg, w, None), "zkie_idft_batch")
+        return d.download().reshape(h, w)
+
+    def lde_batch(self, mat, log_blowup: int, shift: int = 1) -> np.ndarray:
+        m = _as_matrix(mat)
+        h, w = m.shape
+        d_in = DeviceBuffer.from_array(m)
+        d_out = DeviceBuffer((h << log_blowup) * w)
+        check(N.load().zkie_lde_batch(d_in.addr, h, w, log_blowup, shift, d_out.addr, None),
+              "zkie_lde_batch")
+        return d_out.download().reshape(h << log_blowup, w)
+
+
+def lde_device(d_in: DeviceBuffer, h: int, w: int, log_blowup: int, d_out: DeviceBuffer,
+               shift: int = 1, stream=None):
+    check(N.load().zkie_lde_batch(d_in.addr, h, w, log_blowup, shift, d_out.addr, stream),
+          "zkie_lde_batch")
+
+
+class HipMerkleTree:
+    """Prover data of one commitment: the matrix and every digest layer in HBM."""
+
+    def __init__(self, d_mat: DeviceBuffer, h: int, w: int, d_layers: DeviceBuffer, root):
+        self.d_mat, self.h, self.w = d_mat, h, w
+        self.d_layers = d_layers
+        self.layer_lens = N.merkle_layout(h)
+        self.root = np.asarray(root, np.uint64)
+
+    def num_layers(self) -> int:
+        return len(self.layer_lens)
+
+    def layers(self):
+        flat = self.d_layers.download()
+        out, off = [], 0
+        for ln in self.layer_lens:
+            out.append(flat[off:off + 8 * ln].reshape(ln, 8))
+            off += 8 * ln
+        return out
+
+    def matrix(self) -> np.ndarray:
+        return self.d_mat.download(self.h * self.w).reshape(self.h, self.w)
+
+
+class HipMerkleTreeMmcs:
+    """Mmcs<Goldilocks> on the GPU: Poseidon2Goldilocks<16>,
+    PaddingFreeSponge<Perm,16,8,8>, TruncatedPermutation<Perm,2,8,16>, cap 0."""
+
+    def __init__(self, constants=None):
+        if constants is not None:
+            a, b, c, d = constants
+            a, b, c = (np.ascontiguousarray(x, np.uint64) for x in (a, b, c))
+            check(N.load().zkie_p2_upload_constants(N.p(a), N.p(b), N.p(c), d),
+                  "zkie_p2_upload_constants")
+
+    def commit_device(self, d_mat: DeviceBuffer, h: int, w: int, stream=None) -> HipMerkleTree:
+        lens = N.merkle_layout(h)
+        d_layers = DeviceBuffer(sum(lens) * 8)
+        root = np.zeros(8, np.uint64)
+        check(N.load().zkie_merkle_commit(d_mat.addr, h, w, d_layers.addr, N.p(root), stream),
+              "zkie_merkle_commit")
+        return HipMerkleTree(d_mat, h, w, d_layers, root)
+
+    def commit(self, mat) -> tuple[np.ndarray, HipMerkleTree]:
+        m = _as_matrix(mat)
+        h, w = m.shape
+        tree = self.commit_device(DeviceBuffer.from_array(m), h, w)
+        return tree.root, tree
+
+    def open_batch(self, index: int, tree: HipMerkleTree):
+        rows, sib = self.open_batches([index], tree)
+        return rows[0], sib[0]
+
+    def open_batches(self, indices, tree: HipMerkleTree):
+        idx = np.ascontiguousarray(indices, np.uint64)
+        n = idx.size
+        levels = tree.num_layers() - 1
+        rows = np.zeros((n, tree.w), np.uint64)
+        sib = np.zeros((n, max(levels, 0), 8), np.uint64)
+        check(N.load().zkie_merkle_open_batch(
+            tree.d_mat.addr, tree.h, tree.w, tree.d_layers.addr, N.p(idx), n,
+            N.p(rows), N.p(sib) if sib.size else ctypes.cast(0, N._u64p), None),
+            "zkie_merkle_open_batch")
+        return rows, sib
+
+    def open_multi_batch(self, indices, tree: HipMerkleTree):
+        idx = np.ascontiguousarray(indices, np.uint64)
+        n = idx.size
+        rows = np.zeros((n, tree.w), np.uint64)
+        cap = max(1, n * tree.num_layers())
+        out = np.zeros((cap, 8), np.uint64)
+        count = ctypes.c_uint64()
+        check(N.load().zkie_merkle_open_pruned(
+            tree.d_mat.addr, tree.h, tree.w, tree.d_layers.addr, N.p(idx), n, N.p(rows),
+            N.p(out), cap, ctypes.byref(count), None), "zkie_merkle_open_pruned")
+        return rows, out[: count.value]
+
+
+def fold_rows_device(d_mat: DeviceBuffer, h: int, k: int, r, is_ext: bool, d_out: DeviceBuffer,
+                     stream=None):
+    rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
+    assert rr.size == 2 * k
+    check(N.load().zkie_fold_rows(d_mat.addr, h, k, 1 if is_ext else 0, N.p(rr), d_out.addr, stream),
+          "zkie_fold_rows")
+
+
+def fold_rows(mat, k: int, r, is_ext: bool) -> np.ndarray:
+    m = np.ascontiguousarray(np.asarray(mat, np.uint64))
+    h = m.shape[0]
+    d = DeviceBuffer.from_array(m)
+    out = DeviceBuffer(2 * h)
+    fold_rows_device(d, h, k, r, is_ext, out)
+    return out.download().reshape(h, 2)

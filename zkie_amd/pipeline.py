@@ -1,0 +1,96 @@
+"""Device-resident commitment pipelines for the synthetic workloads.
+
+commit_round  <- one WHIR round's encode + commit: p3-whir
+                 src/pcs/committer/writer.rs:21-86 (Suffix order: the table
+                 as coefficient rows of width 2^k, zero-padded by the blowup,
+                 dft_batch per column, Merkle commit of the codeword rows)
+fold          <- the row fold of p3-whir src/pcs/prover/mod.rs:257-290 and the
+                 table fold over the low k variables (common/mle.rs:25-38)
+run_workload  <- the five workloads of zkie_amd.configs, everything in HBM;
+                 only roots, requested openings and checks leave the device.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _native as N
+from .configs import (SEED_CHALLENGES, SEED_DATA, SEED_QUERIES, Workload, XorShift64,
+                      challenges, query_indices)
+from .pcs import HipMerkleTree, HipMerkleTreeMmcs, fold_rows_device, lde_device
+from ._native import DeviceBuffer
+
+
+@dataclass
+class RoundOutput:
+    rows: int                       # codeword rows
+    width: int                      # codeword width in base elements
+    codeword: DeviceBuffer
+    tree: HipMerkleTree
+    queries: np.ndarray | None = None
+    opened_rows: np.ndarray | None = None
+    paths: np.ndarray | None = None
+    pruned: np.ndarray | None = None
+
+
+@dataclass
+class WorkloadOutput:
+    rounds: list = field(default_factory=list)
+    fold: DeviceBuffer | None = None   # row fold of round 0's codeword (configs with fold_k)
+    fold_rows: int = 0
+    tables: list = field(default_factory=list)  # folded tables (config 5), EF flattened
+
+
+def commit_round(d_coeffs: DeviceBuffer, h: int, w: int, log_blowup: int,
+                 mmcs: HipMerkleTreeMmcs, d_codeword: DeviceBuffer | None = None,
+                 stream=None) -> RoundOutput:
+    n = h << log_blowup
+    if d_codeword is None:
+        d_codeword = DeviceBuffer(n * w)
+    lde_device(d_coeffs, h, w, log_blowup, d_codeword, stream=stream)
+    tree = mmcs.commit_device(d_codeword, n, w, stream=stream)
+    return RoundOutput(n, w, d_codeword, tree)
+
+
+def open_round(rnd: RoundOutput, mmcs: HipMerkleTreeMmcs, count: int, g: XorShift64):
+    idx = query_indices(count, rnd.rows, g)
+    rnd.queries = idx
+    rnd.opened_rows, rnd.paths = mmcs.open_batches(idx, rnd.tree)
+    _, rnd.pruned = mmcs.open_multi_batch(idx, rnd.tree)
+
+
+def workload_inputs(wl: Workload) -> np.ndarray:
+    return N.gen_inputs(SEED_DATA, wl.elems, wl.kind).reshape(wl.rows, wl.cols)
+
+
+def run_workload(wl: Workload, d_in: DeviceBuffer, with_openings: bool = True,
+                 stream=None) -> WorkloadOutput:
+    """Run one workload on an input already resident in HBM."""
+    mmcs = HipMerkleTreeMmcs()
+    out = WorkloadOutput()
+    r0 = commit_round(d_in, wl.rows, wl.cols, wl.log_blowup, mmcs, stream=stream)
+    out.rounds.append(r0)
+    k = wl.fold_k
+    if k and wl.rounds == 0:
+        # one fold round over the codeword rows (2^k = width)
+        ch = challenges(k)
+        out.fold = DeviceBuffer(2 * r0.rows)
+        out.fold_rows = r0.rows
+        fold_rows_device(r0.codeword, r0.rows, k, ch, False, out.fold, stream=stream)
+    if wl.rounds:
+        ch = challenges(k * wl.rounds)
+        table, t_rows, ext = d_in, wl.rows, False
+        for r in range(wl.rounds):
+            folded = DeviceBuffer(2 * t_rows)
+            fold_rows_device(table, t_rows, k, ch[k * r:k * (r + 1)], ext, folded, stream=stream)
+            out.tables.append((folded, t_rows))
+            table, ext = folded, True
+            t_rows = t_rows >> k  # EF table of t_rows entries -> rows of 2^k EF
+            rnd = commit_round(folded, t_rows, 2 << k, wl.log_blowup, mmcs, stream=stream)
+            out.rounds.append(rnd)
+    if with_openings and wl.queries:
+        g = XorShift64(SEED_QUERIES)
+        for rnd in out.rounds:
+            open_round(rnd, mmcs, wl.queries, g)
+    return out
