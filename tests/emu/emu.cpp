@@ -16,18 +16,53 @@ using namespace zk;
 
 namespace {
 
-void run_pass(const PassArgs& a, uint32_t T)
+template <int S, int KNZ, bool INV>
+void run_pass_t(const PassArgs& a, uint32_t T)
 {
     const uint64_t blocks = pass_blocks(a);
-    std::vector<uint64_t> lds((size_t)1 << (a.s + a.logC + a.logJ));
+    std::vector<uint64_t> lds(((size_t)1 << (a.s + a.logC + a.logJ)) + 1);
+    constexpr int n = pass_steps<S>();
     for (uint64_t bid = 0; bid < blocks; bid++) {
         const PassTile t = pass_tile(a, bid);
-        if (t.E != lds.size()) std::abort();
-        for (uint32_t tid = 0; tid < T; tid++) pass_load(a, t, tid, T, lds.data());
-        for (int lm = (int)a.s - 1; lm >= 0; lm--)
-            for (uint32_t tid = 0; tid < T; tid++) pass_stage(a, t, lm, tid, T, lds.data());
-        for (uint32_t tid = 0; tid < T; tid++) pass_store(a, t, tid, T, lds.data());
+        for (int k = 0; k < n; k++)  // a barrier separates consecutive steps
+            for (uint32_t tid = 0; tid < T; tid++) pass_step<S, KNZ, INV>(k, a, t, tid, T, lds.data());
     }
+}
+
+template <int S, bool INV>
+void run_pass_s(const PassArgs& a, int knz, uint32_t T)
+{
+    switch (knz) {
+        case 1: run_pass_t<S, 1, INV>(a, T); break;
+        case 2: run_pass_t<S, 2, INV>(a, T); break;
+        case 4: run_pass_t<S, 4, INV>(a, T); break;
+        default: run_pass_t<S, 8, INV>(a, T); break;
+    }
+}
+
+template <bool INV>
+void run_pass_inv(const PassArgs& a, uint32_t T)
+{
+    const int knz = pass_knz(a);
+    switch (a.s) {
+        case 1: run_pass_s<1, INV>(a, knz, T); break;
+        case 2: run_pass_s<2, INV>(a, knz, T); break;
+        case 3: run_pass_s<3, INV>(a, knz, T); break;
+        case 4: run_pass_s<4, INV>(a, knz, T); break;
+        case 5: run_pass_s<5, INV>(a, knz, T); break;
+        case 6: run_pass_s<6, INV>(a, knz, T); break;
+        case 7: run_pass_s<7, INV>(a, knz, T); break;
+        case 8: run_pass_s<8, INV>(a, knz, T); break;
+        default: run_pass_s<9, INV>(a, knz, T); break;
+    }
+}
+
+void run_pass(const PassArgs& a, uint32_t T, bool inverse)
+{
+    if (inverse)
+        run_pass_inv<true>(a, T);
+    else
+        run_pass_inv<false>(a, T);
 }
 
 }  // namespace
@@ -86,14 +121,15 @@ int emu_dft(uint64_t* mat, uint32_t lg, uint64_t w, int inverse, uint32_t thread
     std::vector<uint64_t> tmp(n * w);
     uint32_t B = lg;
     for (uint32_t i = 0; i < p.np; i++) {
-        PassArgs a = pass_args(p, i, B, w, mat, n, tmp.data(), p.np == 1 ? mat : mat, tab.data(), inverse != 0);
+        PassArgs a = pass_args(p, i, B, w, mat, n, tmp.data(), mat, tab.data(), inverse != 0);
         if (p.np == 1) {
-            // single pass in place: emulate the load-all-then-store order
+            // single pass in place: every workgroup reads all its rows before
+            // its last step writes them; a copy of the input stands for that order
             std::vector<uint64_t> src(mat, mat + n * w);
             a.in = src.data();
-            run_pass(a, threads);
+            run_pass(a, threads, inverse != 0);
         } else {
-            run_pass(a, threads);
+            run_pass(a, threads, inverse != 0);
         }
         B -= a.s;
     }
@@ -113,7 +149,7 @@ int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uin
     uint32_t B = L;
     for (uint32_t i = 0; i < p.np; i++) {
         const PassArgs a = pass_args(p, i, B, w, in, h, tmp.data(), out, tab.data(), false);
-        run_pass(a, threads);
+        run_pass(a, threads, false);
         B -= a.s;
     }
     return 0;

@@ -59,7 +59,8 @@ def test_dft_passes(emu, oracle, lg, w):
     assert (y == x).all()
 
 
-@pytest.mark.parametrize("lg,w,lb", [(4, 1, 2), (10, 16, 2), (16, 1, 2), (9, 32, 3), (12, 16, 1)])
+@pytest.mark.parametrize("lg,w,lb", [(4, 1, 2), (10, 16, 2), (16, 1, 2), (9, 32, 3), (12, 16, 1),
+                                     (16, 16, 2), (14, 16, 3), (11, 128, 1), (7, 1, 2), (2, 3, 4)])
 def test_lde_passes(emu, oracle, lg, w, lb):
     x = oracle.gen_uniform(7, (1 << lg) * w).reshape(1 << lg, w)
     out = np.zeros(((1 << lg) << lb, w), np.uint64)

@@ -45,18 +45,49 @@ int ensure_tables(const uint64_t** out)
     return ZKIE_OK;
 }
 
+template <int S, int KNZ, bool INV>
 __global__ __launch_bounds__(256) void ntt_pass_kernel(PassArgs a)
 {
     extern __shared__ uint64_t lds[];
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
     const PassTile t = pass_tile(a, bid);
-    pass_load(a, t, threadIdx.x, blockDim.x, lds);
-    __syncthreads();
-    for (int lm = (int)a.s - 1; lm >= 0; lm--) {
-        pass_stage(a, t, lm, threadIdx.x, blockDim.x, lds);
+    constexpr int n = pass_steps<S>();
+    pass_step<S, KNZ, INV>(0, a, t, threadIdx.x, blockDim.x, lds);
+    if (n > 1) {
         __syncthreads();
+        pass_step<S, KNZ, INV>(1, a, t, threadIdx.x, blockDim.x, lds);
     }
-    pass_store(a, t, threadIdx.x, blockDim.x, lds);
+    if (n > 2) {
+        __syncthreads();
+        pass_step<S, KNZ, INV>(2, a, t, threadIdx.x, blockDim.x, lds);
+    }
+}
+
+template <int S, bool INV>
+void launch_pass_s(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+{
+    switch (knz) {
+        case 1: ntt_pass_kernel<S, 1, INV><<<grid, 256, shmem, s>>>(a); break;
+        case 2: ntt_pass_kernel<S, 2, INV><<<grid, 256, shmem, s>>>(a); break;
+        case 4: ntt_pass_kernel<S, 4, INV><<<grid, 256, shmem, s>>>(a); break;
+        default: ntt_pass_kernel<S, 8, INV><<<grid, 256, shmem, s>>>(a); break;
+    }
+}
+
+template <bool INV>
+void launch_pass(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+{
+    switch (a.s) {
+        case 1: launch_pass_s<1, INV>(a, knz, grid, shmem, s); break;
+        case 2: launch_pass_s<2, INV>(a, knz, grid, shmem, s); break;
+        case 3: launch_pass_s<3, INV>(a, knz, grid, shmem, s); break;
+        case 4: launch_pass_s<4, INV>(a, knz, grid, shmem, s); break;
+        case 5: launch_pass_s<5, INV>(a, knz, grid, shmem, s); break;
+        case 6: launch_pass_s<6, INV>(a, knz, grid, shmem, s); break;
+        case 7: launch_pass_s<7, INV>(a, knz, grid, shmem, s); break;
+        case 8: launch_pass_s<8, INV>(a, knz, grid, shmem, s); break;
+        default: launch_pass_s<9, INV>(a, knz, grid, shmem, s); break;
+    }
 }
 
 // Multiply row j of an h x w matrix by shift^j, shift^j = lo[j & 0xFFFF] * hi[j >> 16].
@@ -92,7 +123,10 @@ int run_passes(const Plan& p, uint64_t w, const uint64_t* in, uint64_t in_rows, 
             grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
         }
         ProfMark m = prof_begin(a.last ? "ntt_pass_last" : "ntt_pass", s);
-        ntt_pass_kernel<<<grid, 256, pass_lds_bytes(a), s>>>(a);
+        if (inverse)
+            launch_pass<true>(a, pass_knz(a), grid, pass_lds_bytes(a), s);
+        else
+            launch_pass<false>(a, pass_knz(a), grid, pass_lds_bytes(a), s);
         prof_end(m, s);
         ZK_LAUNCHED();
         B -= a.s;

@@ -1,16 +1,24 @@
-// One four-step NTT pass, written as phases separated by workgroup barriers
-// so the same code runs in the HIP kernel and in the CPU emulator used by the
-// tests (which executes each phase for every thread of a workgroup in turn
-// and checks every address against its buffer).
+// One four-step NTT pass, written as host/device functions so the same code
+// runs in the HIP kernel and in the CPU emulator used by the tests (which
+// executes each step for every thread of a workgroup in barrier order and
+// checks every address against its buffer).
 //
 // Pass geometry: the array of n = 2^L rows is a set of blocks of N = 2^B
 // rows. A workgroup owns block b, a tile of J = 2^logJ consecutive j2 values
-// and a tile of C = 2^logC columns; it loads the N1 = 2^s points
-// x[b N + j1 N2 + j2][c] (N2 = N / N1) into LDS as lds[j1][v] with
-// v = (j2 - j20) C + (c - c0), runs radix-2 decimation-in-frequency over j1,
+// and a tile of C = 2^logC columns (V = C J vector lanes); it computes the
+// N1 = 2^S point DFT over j1 of x[b N + j1 N2 + j2][c] (N2 = N / N1),
 // multiplies output i1 by w_N^(i1 j2) and stores it at row b N + i1 N2 + j2
-// (or, in the last pass where N2 = 1, at the natural row of position
-// b N1 + i1).
+// (or, in the last pass where N2 = 1, at the natural row of b N1 + i1).
+//
+// The N1-point DFT runs as radix-8/4/2 decimation-in-frequency steps with
+// the small DFTs in registers: step 0 reads its R inputs straight from HBM,
+// intermediate steps exchange through LDS (in place, one barrier between
+// steps), and the last step writes straight to HBM. Step t works on
+// sub-problems of 2^BS points: for each (blk, q < 2^(BS - r), v) it loads the
+// R = 2^r points q + k 2^(BS - r), computes their R-point DFT, multiplies
+// frequency f by w_{2^BS}^(f q) and stores it at q + f 2^(BS - r). After the
+// last step, position pos = f_0 2^(S - r_0) + f_1 2^(S - r_0 - r_1) + ... holds
+// frequency i1 = f_0 + f_1 2^(r_0) + ... (mixed-radix digit reversal).
 #pragma once
 
 #include "gl64.hpp"
@@ -34,13 +42,15 @@
 
 namespace zk {
 
+constexpr int kStepTableLg = 9;  // in-pass twiddles come from w_512^k, k < 512
+
 struct PassArgs {
     const uint64_t* in;
     uint64_t* out;
     uint64_t in_rows;  // rows of `in` holding data; rows beyond read as zero
     uint64_t w;
-    uint64_t scale;  // last pass: multiply by this (1 = forward)
-    const uint64_t* tws;   // small tables: w_{2^lg}^k at offset 2^(lg-1) - 1
+    uint64_t scale;        // last pass: multiply by this (1 = forward)
+    const uint64_t* w512;  // w_512^k, k < 512 (forward or inverse)
     const uint64_t* twlo;  // w_{2^32}^x, x < 2^16
     const uint64_t* twhi;  // w_{2^32}^(x 2^16), x < 2^16
     uint64_t in_len, out_len;  // element counts, checked by the emulator only
@@ -56,7 +66,7 @@ struct PassTile {
     uint64_t c0;   // first column
     uint64_t j20;  // first j2
     uint64_t N2;
-    uint32_t logV, E;
+    uint32_t logV;
 };
 
 __host__ __device__ __forceinline__ uint32_t bit_reverse(uint32_t x, uint32_t bits)
@@ -84,7 +94,6 @@ __host__ __device__ __forceinline__ PassTile pass_tile(const PassArgs& a, uint64
     t.c0 = ct << a.logC;
     t.j20 = jt << a.logJ;
     t.logV = a.logC + a.logJ;
-    t.E = (1u << a.s) << t.logV;
     return t;
 }
 
@@ -108,67 +117,207 @@ __host__ __device__ __forceinline__ uint64_t pass_natural_row(const PassArgs& a,
     return nat;
 }
 
-__host__ __device__ __forceinline__ void pass_load(const PassArgs& a, const PassTile& t, uint32_t tid,
-                                                   uint32_t T, uint64_t* lds)
+// Radix decomposition of an S-point sub-DFT: digits r_0, r_1, r_2 (bits).
+template <int S>
+struct Radix {
+    static constexpr int n = S <= 3 ? 1 : (S <= 6 ? 2 : 3);
+    static constexpr int r0 = S <= 3 ? S : 3;
+    static constexpr int r1 = S <= 3 ? 0 : (S <= 6 ? S - 3 : (S == 7 ? 2 : 3));
+    static constexpr int r2 = S - r0 - r1;
+};
+// S=9: 3,3,3  S=8: 3,3,2  S=7: 3,2,2  S=6: 3,3  S=5: 3,2  S=4: 3,1 ... all digits <= 3.
+
+// Frequency of position pos for the digit sequence of Radix<S>.
+template <int S>
+__host__ __device__ __forceinline__ uint32_t digit_reverse(uint32_t pos)
 {
-    const uint32_t V = 1u << t.logV;
-    const uint32_t cmask = (1u << a.logC) - 1;
-    for (uint32_t e = tid; e < t.E; e += T) {
-        const uint32_t i = e >> t.logV, v = e & (V - 1);
-        const uint64_t row = t.blk + (uint64_t)i * t.N2 + t.j20 + (v >> a.logC);
-        uint64_t x = 0;
-        if (row < a.in_rows) {
-            const uint64_t idx = row * a.w + t.c0 + (v & cmask);
-            ZK_BOUND(idx, a.in_len);
-            x = a.in[idx];
+    using Rd = Radix<S>;
+    uint32_t f = 0, sh = 0, rem = S;
+    rem -= Rd::r0;
+    f |= ((pos >> rem) & ((1u << Rd::r0) - 1)) << sh;
+    sh += Rd::r0;
+    if (Rd::r1) {
+        rem -= Rd::r1;
+        f |= ((pos >> rem) & ((1u << Rd::r1) - 1)) << sh;
+        sh += Rd::r1;
+    }
+    if (Rd::r2) {
+        rem -= Rd::r2;
+        f |= ((pos >> rem) & ((1u << Rd::r2) - 1)) << sh;
+    }
+    return f;
+}
+
+// Roots of unity used inside the 8- and 4-point DFTs.
+template <bool INV>
+struct SmallRoots {
+    static constexpr uint64_t w4 = INV ? 0xFFFEFFFF00000001ull : 0x0001000000000000ull;
+    static constexpr uint64_t w8 = INV ? 0x000000FFFFFFFF00ull : 0xFFFFFFFEFF000001ull;
+    static constexpr uint64_t w8_3 = INV ? 0x0000000001000000ull : 0xFFFFFEFF00000101ull;
+};
+
+// In-register R-point DFT (radix-2 DIF); x[idx] ends up holding frequency
+// bit_reverse(idx, log2 R).
+template <int RLOG, bool INV>
+__host__ __device__ __forceinline__ void dft_small(uint64_t* x)
+{
+    using W = SmallRoots<INV>;
+    if (RLOG == 3) {
+        const uint64_t tw[4] = {1, W::w8, W::w4, W::w8_3};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint64_t u = x[p], v = x[p + 4];
+            x[p] = gl_add(u, v);
+            const uint64_t d = gl_sub(u, v);
+            x[p + 4] = p == 0 ? d : gl_mul(d, tw[p]);
         }
-        lds[e] = x;
+#pragma unroll
+        for (int h = 0; h < 8; h += 4) {
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const uint64_t u = x[h + p], v = x[h + p + 2];
+                x[h + p] = gl_add(u, v);
+                const uint64_t d = gl_sub(u, v);
+                x[h + p + 2] = p == 0 ? d : gl_mul(d, W::w4);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q += 2) {
+            const uint64_t u = x[q], v = x[q + 1];
+            x[q] = gl_add(u, v);
+            x[q + 1] = gl_sub(u, v);
+        }
+    } else if (RLOG == 2) {
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint64_t u = x[p], v = x[p + 2];
+            x[p] = gl_add(u, v);
+            const uint64_t d = gl_sub(u, v);
+            x[p + 2] = p == 0 ? d : gl_mul(d, W::w4);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+            const uint64_t u = x[q], v = x[q + 1];
+            x[q] = gl_add(u, v);
+            x[q + 1] = gl_sub(u, v);
+        }
+    } else if (RLOG == 1) {
+        const uint64_t u = x[0], v = x[1];
+        x[0] = gl_add(u, v);
+        x[1] = gl_sub(u, v);
     }
 }
 
-// Radix-2 DIF stage with half-size m = 2^lm over the N1 points of every v.
-__host__ __device__ __forceinline__ void pass_stage(const PassArgs& a, const PassTile& t, int lm,
-                                                    uint32_t tid, uint32_t T, uint64_t* lds)
+// Global source element j1 (within the block), vector lane v.
+__host__ __device__ __forceinline__ uint64_t pass_load_elem(const PassArgs& a, const PassTile& t,
+                                                            uint32_t j1, uint32_t v)
 {
-    const uint32_t V = 1u << t.logV;
-    const uint32_t nbf = t.E >> 1;
-    const uint32_t m = 1u << lm;
-    for (uint32_t q = tid; q < nbf; q += T) {
-        const uint32_t v = q & (V - 1), k = q >> t.logV;
-        const uint32_t pos = k & (m - 1);
-        const uint32_t i0 = ((k >> lm) << (lm + 1)) | pos;
-        const uint32_t x0 = (i0 << t.logV) | v, x1 = ((i0 + m) << t.logV) | v;
-        ZK_BOUND(x1, t.E);
-        const uint64_t u = lds[x0], w = lds[x1];
-        lds[x0] = gl_add(u, w);
-        const uint64_t d = gl_sub(u, w);
-        lds[x1] = lm ? gl_mul(d, a.tws[(m - 1) + pos]) : d;
+    const uint64_t row = t.blk + (uint64_t)j1 * t.N2 + t.j20 + (v >> a.logC);
+    if (row >= a.in_rows) return 0;
+    const uint64_t idx = row * a.w + t.c0 + (v & ((1u << a.logC) - 1));
+    ZK_BOUND(idx, a.in_len);
+    return a.in[idx];
+}
+
+// Global destination of frequency i1, vector lane v (inter-pass twiddle,
+// last-pass scale and canonical form applied here).
+__host__ __device__ __forceinline__ void pass_store_elem(const PassArgs& a, const PassTile& t,
+                                                         uint32_t i1, uint32_t v, uint64_t val)
+{
+    const uint64_t c = t.c0 + (v & ((1u << a.logC) - 1));
+    if (!a.last) {
+        const uint64_t j2 = t.j20 + (v >> a.logC);
+        const uint64_t ex = (uint64_t)i1 * j2;
+        if (ex) val = gl_mul(val, pass_root_pow(a, ex));
+        const uint64_t idx = (t.blk + (uint64_t)i1 * t.N2 + j2) * a.w + c;
+        ZK_BOUND(idx, a.out_len);
+        a.out[idx] = val;
+    } else {
+        if (a.scale != 1) val = gl_mul(val, a.scale);
+        const uint64_t idx = pass_natural_row(a, t.blk + i1) * a.w + c;
+        ZK_BOUND(idx, a.out_len);
+        a.out[idx] = gl_canon(val);
     }
 }
 
-__host__ __device__ __forceinline__ void pass_store(const PassArgs& a, const PassTile& t, uint32_t tid,
-                                                    uint32_t T, const uint64_t* lds)
+// One radix-2^RL DIF step on sub-problems of 2^BS points of an S-point DFT.
+// FROM_GLOBAL: inputs from HBM (step 0; only the first KNZ of the R inputs
+// can be non-zero, the rest are the zero padding of an LDE). TO_GLOBAL:
+// outputs to HBM (last step).
+template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL>
+__host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, uint32_t tid,
+                                                  uint32_t T, uint64_t* lds)
 {
-    const uint32_t V = 1u << t.logV;
-    const uint32_t cmask = (1u << a.logC) - 1;
-    for (uint32_t e = tid; e < t.E; e += T) {
-        const uint32_t pos = e >> t.logV, v = e & (V - 1);
-        const uint32_t i1 = bit_reverse(pos, a.s);
-        uint64_t val = lds[e];
-        const uint64_t c = t.c0 + (v & cmask);
-        if (!a.last) {
-            const uint64_t j2 = t.j20 + (v >> a.logC);
-            const uint64_t ex = (uint64_t)i1 * j2;
-            if (ex) val = gl_mul(val, pass_root_pow(a, ex));
-            const uint64_t idx = (t.blk + (uint64_t)i1 * t.N2 + j2) * a.w + c;
-            ZK_BOUND(idx, a.out_len);
-            a.out[idx] = val;
-        } else {
-            if (a.scale != 1) val = gl_mul(val, a.scale);
-            const uint64_t idx = pass_natural_row(a, t.blk + i1) * a.w + c;
-            ZK_BOUND(idx, a.out_len);
-            a.out[idx] = gl_canon(val);
+    constexpr int R = 1 << RL;
+    constexpr int QL = BS - RL;
+    const uint32_t logV = t.logV;
+    const uint32_t V = 1u << logV;
+    const uint32_t items = (1u << (S - RL)) << logV;
+    for (uint32_t it = tid; it < items; it += T) {
+        const uint32_t v = it & (V - 1);
+        const uint32_t rest = it >> logV;
+        const uint32_t q = rest & ((1u << QL) - 1);
+        const uint32_t base = ((rest >> QL) << BS) + q;
+        uint64_t x[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            const uint32_t pos = base + ((uint32_t)k << QL);
+            if (FROM_GLOBAL) {
+                x[k] = k < KNZ ? pass_load_elem(a, t, pos, v) : 0;
+            } else {
+                ZK_BOUND((pos << logV) | v, (1u << S) << logV);
+                x[k] = lds[(pos << logV) | v];
+            }
         }
+        dft_small<RL, INV>(x);
+        if (QL > 0 && q != 0) {
+#pragma unroll
+            for (int idx = 1; idx < R; idx++) {
+                const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                x[idx] = gl_mul(x[idx], a.w512[(f * q) << (kStepTableLg - BS)]);
+            }
+        }
+#pragma unroll
+        for (int idx = 0; idx < R; idx++) {
+            const uint32_t f = bit_reverse((uint32_t)idx, RL);
+            const uint32_t pos = base + (f << QL);
+            if (TO_GLOBAL) {
+                pass_store_elem(a, t, digit_reverse<S>(pos), v, x[idx]);
+            } else {
+                ZK_BOUND((pos << logV) | v, (1u << S) << logV);
+                lds[(pos << logV) | v] = x[idx];
+            }
+        }
+    }
+}
+
+// Number of barrier-separated steps of an S-point sub-DFT.
+template <int S>
+constexpr int pass_steps()
+{
+    return Radix<S>::n;
+}
+
+// Step `k` of the S-point sub-DFT (k < pass_steps<S>()). The caller puts a
+// workgroup barrier between consecutive steps.
+template <int S, int KNZ, bool INV>
+__host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, const PassTile& t,
+                                                   uint32_t tid, uint32_t T, uint64_t* lds)
+{
+    using Rd = Radix<S>;
+    constexpr int n = Rd::n;
+    if (k == 0) {
+        if (n == 1)
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, true>(a, t, tid, T, lds);
+        else
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, false>(a, t, tid, T, lds);
+    } else if (k == 1) {
+        if (n == 2)
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true>(a, t, tid, T, lds);
+        else if (n == 3)
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false>(a, t, tid, T, lds);
+    } else if (k == 2) {
+        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true>(a, t, tid, T, lds);
     }
 }
 

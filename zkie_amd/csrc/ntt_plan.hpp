@@ -9,14 +9,13 @@
 namespace zk {
 
 constexpr uint32_t kMaxPassBits = 9;
-constexpr uint32_t kSmallLg = 13;                 // small tables: w_{2^lg}, lg <= 13
-constexpr uint64_t kSmallLen = 1ull << kSmallLg;  // one table, offsets 2^(lg-1) - 1
-constexpr uint64_t kBigLen = 1ull << 16;          // two-level table of w_{2^32}
-constexpr uint64_t kTableLen = 2 * kSmallLen + 4 * kBigLen;
+constexpr uint64_t kW512Len = 1ull << kStepTableLg;  // w_512^k, k < 512
+constexpr uint64_t kBigLen = 1ull << 16;             // two-level table of w_{2^32}
+constexpr uint64_t kTableLen = 2 * kW512Len + 4 * kBigLen;
 
-// Table layout: [small_fwd | small_inv | lo_fwd | hi_fwd | lo_inv | hi_inv].
-inline const uint64_t* tab_small(const uint64_t* base, bool inv) { return base + (inv ? kSmallLen : 0); }
-inline const uint64_t* tab_lo(const uint64_t* base, bool inv) { return base + 2 * kSmallLen + (inv ? 2 * kBigLen : 0); }
+// Table layout: [w512_fwd | w512_inv | lo_fwd | hi_fwd | lo_inv | hi_inv].
+inline const uint64_t* tab_w512(const uint64_t* base, bool inv) { return base + (inv ? kW512Len : 0); }
+inline const uint64_t* tab_lo(const uint64_t* base, bool inv) { return base + 2 * kW512Len + (inv ? 2 * kBigLen : 0); }
 inline const uint64_t* tab_hi(const uint64_t* base, bool inv) { return tab_lo(base, inv) + kBigLen; }
 
 // TWO_ADIC_GENERATORS[k] = 7^((p-1)/2^k), the table dft_cuda.rs:49 reads.
@@ -26,22 +25,19 @@ inline std::vector<uint64_t> build_twiddle_tables()
 {
     std::vector<uint64_t> h(kTableLen, 0);
     for (int inv = 0; inv < 2; inv++) {
-        uint64_t* sm = h.data() + (inv ? kSmallLen : 0);
-        for (uint32_t lg = 1; lg <= kSmallLg; lg++) {
-            uint64_t root = two_adic_generator(lg);
-            if (inv) root = gl_inv(root);
-            const uint64_t off = (1ull << (lg - 1)) - 1;
-            uint64_t x = 1;
-            for (uint64_t k = 0; k < (1ull << (lg - 1)); k++) {
-                sm[off + k] = x;
-                x = gl_canon(gl_mul(x, root));
-            }
+        uint64_t* w512 = h.data() + (inv ? kW512Len : 0);
+        uint64_t root = two_adic_generator(kStepTableLg);
+        if (inv) root = gl_inv(root);
+        uint64_t x = 1;
+        for (uint64_t k = 0; k < kW512Len; k++) {
+            w512[k] = x;
+            x = gl_canon(gl_mul(x, root));
         }
         uint64_t g32 = two_adic_generator(32);
         if (inv) g32 = gl_inv(g32);
-        uint64_t* lo = h.data() + 2 * kSmallLen + (inv ? 2 * kBigLen : 0);
+        uint64_t* lo = h.data() + 2 * kW512Len + (inv ? 2 * kBigLen : 0);
         uint64_t* hi = lo + kBigLen;
-        uint64_t x = 1;
+        x = 1;
         for (uint64_t k = 0; k < kBigLen; k++) {
             lo[k] = x;
             x = gl_canon(gl_mul(x, g32));
@@ -88,7 +84,7 @@ inline PassArgs pass_args(const Plan& p, uint32_t i, uint32_t B, uint64_t w, con
     a.in_rows = i == 0 ? in_rows : n;
     a.w = w;
     a.scale = last && inverse ? gl_inv(n % P) : 1;
-    a.tws = tab_small(tables, inverse);
+    a.w512 = tab_w512(tables, inverse);
     a.twlo = tab_lo(tables, inverse);
     a.twhi = tab_hi(tables, inverse);
     a.in_len = (i == 0 ? in_rows : n) * w;
@@ -107,6 +103,31 @@ inline PassArgs pass_args(const Plan& p, uint32_t i, uint32_t B, uint64_t w, con
     return a;
 }
 
-inline size_t pass_lds_bytes(const PassArgs& a) { return ((size_t)1 << (a.s + a.logC + a.logJ)) * 8; }
+// LDS of a pass: the N1 x V tile, unless the sub-DFT is a single step.
+inline size_t pass_lds_bytes(const PassArgs& a)
+{
+    return a.s <= 3 ? 0 : ((size_t)1 << (a.s + a.logC + a.logJ)) * 8;
+}
+
+// Non-zero inputs among the R = 2^r0 inputs of a step-0 radix DFT: an LDE's
+// first pass reads h = n / blowup rows, so inputs k >= R / blowup are zero.
+inline int pass_knz(const PassArgs& a)
+{
+    const int r0 = a.s <= 3 ? (int)a.s : 3;
+    const uint64_t n = 1ull << a.L;
+    const uint64_t R = 1ull << r0;
+    if (a.in_rows >= n || a.B != a.L) return (int)R;
+    // rows j1 N2 + j2 < in_rows <=> j1 < in_rows / N2 (a power of two here)
+    const uint64_t n2 = 1ull << (a.B - a.s);
+    const uint64_t j1_nz = (a.in_rows + n2 - 1) / n2;  // j1 < j1_nz can be non-zero
+    const uint64_t q_span = 1ull << (a.s - r0);
+    uint64_t knz = (j1_nz + q_span - 1) / q_span;
+    if (knz > R) knz = R;
+    if (knz < 1) knz = 1;
+    // round up to a power of two (template instances exist for 1, 2, 4, 8)
+    uint64_t p2 = 1;
+    while (p2 < knz) p2 <<= 1;
+    return (int)p2;
+}
 
 }  // namespace zk
