@@ -46,6 +46,7 @@ def lib():
             "or_idft_batch": (None, [_u64p, u32, u64]),
             "or_dft_naive": (None, [_u64p, _u64p, u32, u64]),
             "or_poly_eval": (u64, [_u64p, u64, u64, u64, u64]),
+            "or_checksum": (u64, [_u64p, u64, u64]),
             "or_lde_batch": (None, [_u64p, u64, u64, u32, u64, _u64p]),
             "or_p2_derive_constants": (None, [_u64p, _u64p, _u64p, _u64p]),
             "or_p2_set_constants": (None, [_u64p, _u64p, _u64p, u64]),
@@ -143,6 +144,15 @@ def poly_eval(mat: np.ndarray, c: int, x: int) -> int:
     m = u64(mat)
     h, w = m.shape
     return lib().or_poly_eval(_p(m), h, w, c, x)
+
+
+CHECKSUM_Z = 0x1BADB002DEADBEEF
+
+
+def checksum(v: np.ndarray, z: int = CHECKSUM_Z) -> int:
+    """sum_i v[i] z^i mod p over the flattened array."""
+    a = u64(v).reshape(-1)
+    return lib().or_checksum(_p(a), a.size, z)
 
 
 def lde_batch(mat: np.ndarray, log_blowup: int, shift: int = 1) -> np.ndarray:

@@ -156,6 +156,14 @@ uint64_t or_poly_eval(const uint64_t *mat, uint64_t h, uint64_t w, uint64_t c, u
     return acc;
 }
 
+/* Polynomial checksum sum_i v[i] z^i (Horner), a fingerprint of a vector. */
+uint64_t or_checksum(const uint64_t *v, uint64_t n, uint64_t z)
+{
+    uint64_t acc = 0;
+    for (uint64_t i = n; i-- > 0;) acc = or_add(or_mul(acc, z), v[i] % OR_P);
+    return acc;
+}
+
 void or_dft_naive(const uint64_t *in, uint64_t *out, uint32_t lg_h, uint64_t w)
 {
     const uint64_t h = 1ULL << lg_h;

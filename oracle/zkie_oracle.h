@@ -41,6 +41,8 @@ void or_dft_batch(uint64_t *mat, uint32_t lg_h, uint64_t w);
 void or_dft_naive(const uint64_t *in, uint64_t *out, uint32_t lg_h, uint64_t w);
 /* Horner evaluation of column c of an h x w coefficient matrix at x. */
 uint64_t or_poly_eval(const uint64_t *mat, uint64_t h, uint64_t w, uint64_t c, uint64_t x);
+/* Polynomial fingerprint sum_i v[i] z^i mod p. */
+uint64_t or_checksum(const uint64_t *v, uint64_t n, uint64_t z);
 /* Inverse DFT (evaluations -> coefficients), in place. */
 void or_idft_batch(uint64_t *mat, uint32_t lg_h, uint64_t w);
 /* WHIR encode / LDE (p3-whir writer.rs:73-81): zero-pad the h x w coefficient

@@ -91,6 +91,13 @@ uint64_t emu_acc_sum(const uint64_t* x, uint64_t n)
     return acc_reduce(a);
 }
 uint64_t emu_gl_canon(uint64_t a) { return gl_canon(a); }
+uint64_t emu_gl_canon_fast(uint64_t a) { return gl_canon_fast(a); }
+uint64_t emu_gl_shl(uint64_t a, int s) { return s == 1 ? gl_shl<1>(a) : gl_shl<2>(a); }
+uint64_t emu_gl_add_shl(uint64_t sum, uint64_t a, int s)
+{
+    return s == 1 ? gl_add_shl<1>(sum, a) : gl_add_shl<2>(sum, a);
+}
+uint64_t emu_gl_add_small(uint64_t a, uint64_t b) { return gl_add_small(a, b); }
 
 // Permutation with explicit constants (layout of zkie_p2_upload_constants).
 void emu_p2_permute(uint64_t* st, const uint64_t* rc_init, const uint64_t* rc_final,

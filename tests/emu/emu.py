@@ -33,7 +33,14 @@ def load():
         for n in ("emu_gl_add", "emu_gl_sub", "emu_gl_mul"):
             getattr(L, n).restype = _u64
             getattr(L, n).argtypes = [_u64, _u64]
-        for n in ("emu_gl_sqr", "emu_gl_halve", "emu_gl_canon"):
+        for n in ("emu_gl_add_small",):
+            getattr(L, n).restype = _u64
+            getattr(L, n).argtypes = [_u64, _u64]
+        L.emu_gl_shl.restype = _u64
+        L.emu_gl_shl.argtypes = [_u64, ctypes.c_int]
+        L.emu_gl_add_shl.restype = _u64
+        L.emu_gl_add_shl.argtypes = [_u64, _u64, ctypes.c_int]
+        for n in ("emu_gl_sqr", "emu_gl_halve", "emu_gl_canon", "emu_gl_canon_fast"):
             getattr(L, n).restype = _u64
             getattr(L, n).argtypes = [_u64]
         L.emu_gl_inv_pow2.restype = _u64

@@ -26,6 +26,12 @@ def test_arithmetic(emu):
         assert emu.emu_gl_canon(emu.emu_gl_halve(a)) == a * pow(2, P - 2, P) % P
         for k in (3, 4, 5, 32):
             assert emu.emu_gl_canon(emu.emu_gl_inv_pow2(a, k)) == a * pow(2**k, P - 2, P) % P
+        assert emu.emu_gl_canon_fast(a) == a % P
+        for sh in (1, 2):
+            assert emu.emu_gl_canon(emu.emu_gl_shl(a, sh)) == (a << sh) % P
+            assert emu.emu_gl_canon(emu.emu_gl_add_shl(b, a, sh)) == (b + (a << sh)) % P
+        if b < P:
+            assert emu.emu_gl_canon(emu.emu_gl_add_small(a, b)) == (a + b) % P
     for n in (1, 16, 36, 1000):
         x = np.array([rng.getrandbits(64) for _ in range(n)], np.uint64)
         assert emu.emu_gl_canon(emu.emu_acc_sum(ptr(x), n)) == sum(int(v) for v in x) % P

@@ -114,6 +114,36 @@ __host__ __device__ __forceinline__ uint64_t gl_mul_inv_pow2(uint64_t x)
     return gl_add_small(q, y) ;
 }
 
+// Canonical representative: x >= p exactly when x + eps wraps.
+__host__ __device__ __forceinline__ uint64_t gl_canon_fast(uint64_t x)
+{
+    const uint64_t t = x + EPS;
+    return t < x ? t : x;
+}
+
+// x * 2^S for S in {1, 2}: lo + k 2^64 with k < 2^S, and k eps < p folds in
+// with one wrap at most.
+template <int S>
+__host__ __device__ __forceinline__ uint64_t gl_shl(uint64_t x)
+{
+    static_assert(S >= 1 && S <= 2, "shift range");
+    const uint64_t lo = x << S;
+    const uint64_t r = lo + (x >> (64 - S)) * EPS;
+    return r + (r < lo ? EPS : 0);
+}
+
+// sum + x * 2^S for S in {1, 2}: the two wraps (shifted-out bits and the
+// addition carry) are counted into k <= 2^S, then k eps folds in once.
+template <int S>
+__host__ __device__ __forceinline__ uint64_t gl_add_shl(uint64_t sum, uint64_t x)
+{
+    static_assert(S >= 1 && S <= 2, "shift range");
+    const uint64_t lo = (x << S) + sum;
+    const uint64_t k = (x >> (64 - S)) + (lo < sum ? 1 : 0);
+    const uint64_t r = lo + k * EPS;
+    return r + (r < lo ? EPS : 0);
+}
+
 __host__ __device__ __forceinline__ uint64_t gl_halve(uint64_t x)
 {
     return (x >> 1) + ((x & 1) ? HALF : 0);

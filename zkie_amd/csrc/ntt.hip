@@ -46,7 +46,7 @@ int ensure_tables(const uint64_t** out)
 }
 
 template <int S, int KNZ, bool INV>
-__global__ __launch_bounds__(256) void ntt_pass_kernel(PassArgs a)
+__global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 {
     extern __shared__ uint64_t lds[];
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
@@ -67,10 +67,10 @@ template <int S, bool INV>
 void launch_pass_s(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
 {
     switch (knz) {
-        case 1: ntt_pass_kernel<S, 1, INV><<<grid, 256, shmem, s>>>(a); break;
-        case 2: ntt_pass_kernel<S, 2, INV><<<grid, 256, shmem, s>>>(a); break;
-        case 4: ntt_pass_kernel<S, 4, INV><<<grid, 256, shmem, s>>>(a); break;
-        default: ntt_pass_kernel<S, 8, INV><<<grid, 256, shmem, s>>>(a); break;
+        case 1: ntt_pass_kernel<S, 1, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
+        case 2: ntt_pass_kernel<S, 2, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
+        case 4: ntt_pass_kernel<S, 4, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
+        default: ntt_pass_kernel<S, 8, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
     }
 }
 

@@ -9,6 +9,12 @@
 namespace zk {
 
 constexpr uint32_t kMaxPassBits = 9;
+// Threads of a pass workgroup: a 512 x 16 tile (64 KB of LDS) with 512
+// threads keeps four waves per SIMD on a CU holding two such workgroups.
+#ifndef ZK_NTT_THREADS
+#define ZK_NTT_THREADS 512
+#endif
+constexpr uint32_t kNttThreads = ZK_NTT_THREADS;
 constexpr uint64_t kW512Len = 1ull << kStepTableLg;  // w_512^k, k < 512
 constexpr uint64_t kBigLen = 1ull << 16;             // two-level table of w_{2^32}
 constexpr uint64_t kTableLen = 2 * kW512Len + 4 * kBigLen;

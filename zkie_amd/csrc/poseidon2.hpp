@@ -15,7 +15,11 @@
 //    once per output, instead of reducing after every addition, and the next
 //    round's constants are folded into that same reduction;
 //  * 1/2^k multiplies are shift/add sequences (gl_mul_inv_pow2), and the
-//    2^-32 entry uses the same closed form when diag15 has that value;
+//    2^-32 entry uses the same closed form when diag15 has that value; 2x,
+//    3x and 4x are shifts with the wrapped bits folded back once;
+//  * in the internal rounds the work that does not depend on the S-box is
+//    issued before it, and the round sum is made canonical so the sixteen
+//    "sum + t" additions need one wrap correction each;
 //  * round loops stay rolled (one copy of the external round body) to keep
 //    the code inside the instruction cache.
 #pragma once
@@ -71,33 +75,48 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
     }
 }
 
+// One internal round: st0 <- (st0 + rc)^7, then st_i <- sum + V_i st_i.
+// The 15 scaled terms and the partial sum of st[1..15] do not depend on the
+// S-box, so they are formed first; the full sum is made canonical so that
+// every "sum + t" below needs a single wrap correction.
 template <bool DIAG15_IS_INV_2_32>
-__host__ __device__ __forceinline__ void internal_linear(uint64_t* st, uint64_t diag15)
+__host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t rc, uint64_t diag15)
 {
-    Acc s = acc_of(st[0]);
+    Acc s = acc_of(st[1]);
 #pragma unroll
-    for (int i = 1; i < 16; i++) s = acc_add(s, st[i]);
-    const uint64_t sum = acc_reduce(s);
-    const uint64_t x0 = st[0];
-    st[0] = gl_sub(sum, gl_double(x0));                       // -2
-    st[1] = gl_add(sum, st[1]);                               // 1
-    st[2] = gl_add(sum, gl_double(st[2]));                    // 2
-    st[3] = gl_add(sum, gl_halve(st[3]));                     // 1/2
-    st[4] = gl_add(sum, gl_add(gl_double(st[4]), st[4]));     // 3
-    st[5] = gl_add(sum, gl_double(gl_double(st[5])));         // 4
-    st[6] = gl_sub(sum, gl_halve(st[6]));                     // -1/2
-    st[7] = gl_sub(sum, gl_add(gl_double(st[7]), st[7]));     // -3
-    st[8] = gl_sub(sum, gl_double(gl_double(st[8])));         // -4
-    st[9] = gl_add(sum, gl_mul_inv_pow2<3>(st[9]));           // 1/2^3
-    st[10] = gl_add(sum, gl_mul_inv_pow2<4>(st[10]));         // 1/2^4
-    st[11] = gl_add(sum, gl_mul_inv_pow2<5>(st[11]));         // 1/2^5
-    st[12] = gl_sub(sum, gl_mul_inv_pow2<3>(st[12]));         // -1/2^3
-    st[13] = gl_sub(sum, gl_mul_inv_pow2<4>(st[13]));         // -1/2^4
-    st[14] = gl_sub(sum, gl_mul_inv_pow2<5>(st[14]));         // -1/2^5
-    if (DIAG15_IS_INV_2_32)
-        st[15] = gl_add(sum, gl_mul_inv_pow2<32>(st[15]));
-    else
-        st[15] = gl_add(sum, gl_mul(st[15], diag15));
+    for (int i = 2; i < 16; i++) s = acc_add(s, st[i]);
+    const uint64_t t2 = gl_shl<1>(st[2]);                    //  2
+    const uint64_t t3 = gl_halve(st[3]);                     //  1/2
+    const uint64_t t4 = gl_add_shl<1>(st[4], st[4]);         //  3
+    const uint64_t t5 = gl_shl<2>(st[5]);                    //  4
+    const uint64_t t6 = gl_halve(st[6]);                     // -1/2
+    const uint64_t t7 = gl_add_shl<1>(st[7], st[7]);         // -3
+    const uint64_t t8 = gl_shl<2>(st[8]);                    // -4
+    const uint64_t t9 = gl_mul_inv_pow2<3>(st[9]);           //  1/2^3
+    const uint64_t t10 = gl_mul_inv_pow2<4>(st[10]);         //  1/2^4
+    const uint64_t t11 = gl_mul_inv_pow2<5>(st[11]);         //  1/2^5
+    const uint64_t t12 = gl_mul_inv_pow2<3>(st[12]);         // -1/2^3
+    const uint64_t t13 = gl_mul_inv_pow2<4>(st[13]);         // -1/2^4
+    const uint64_t t14 = gl_mul_inv_pow2<5>(st[14]);         // -1/2^5
+    const uint64_t t15 = DIAG15_IS_INV_2_32 ? gl_mul_inv_pow2<32>(st[15]) : gl_mul(st[15], diag15);
+    const uint64_t x0 = sbox7(gl_add_small(st[0], rc));
+    const uint64_t sum = gl_canon_fast(acc_reduce(acc_add(s, x0)));
+    st[0] = gl_sub(sum, gl_shl<1>(x0));                      // -2
+    st[1] = gl_add_small(st[1], sum);                        //  1
+    st[2] = gl_add_small(t2, sum);
+    st[3] = gl_add_small(t3, sum);
+    st[4] = gl_add_small(t4, sum);
+    st[5] = gl_add_small(t5, sum);
+    st[6] = gl_sub(sum, t6);
+    st[7] = gl_sub(sum, t7);
+    st[8] = gl_sub(sum, t8);
+    st[9] = gl_add_small(t9, sum);
+    st[10] = gl_add_small(t10, sum);
+    st[11] = gl_add_small(t11, sum);
+    st[12] = gl_sub(sum, t12);
+    st[13] = gl_sub(sum, t13);
+    st[14] = gl_sub(sum, t14);
+    st[15] = gl_add_small(t15, sum);                         //  diag15
 }
 
 template <bool DIAG15_IS_INV_2_32>
@@ -112,10 +131,7 @@ __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts
         if (r == 3) {
             mds_light16<false>(st, nullptr);
 #pragma unroll 1
-            for (int k = 0; k < 22; k++) {
-                st[0] = sbox7(gl_add_small(st[0], C.internal[k]));
-                internal_linear<DIAG15_IS_INV_2_32>(st, C.diag15);
-            }
+            for (int k = 0; k < 22; k++) internal_round<DIAG15_IS_INV_2_32>(st, C.internal[k], C.diag15);
             // Constants of the first terminal round (st += rc) before its S-box.
 #pragma unroll
             for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
