@@ -20,10 +20,11 @@ template <int S, int KNZ, bool INV>
 void run_pass_t(const PassArgs& a, uint32_t T)
 {
     const uint64_t blocks = pass_blocks(a);
-    std::vector<uint64_t> lds(((size_t)1 << (a.s + a.logC + a.logJ)) + 1);
+    std::vector<uint64_t> lds(pass_lds_bytes(a) / 8 + 1);
     constexpr int n = pass_steps<S>();
     for (uint64_t bid = 0; bid < blocks; bid++) {
         const PassTile t = pass_tile(a, bid);
+        for (uint32_t tid = 0; tid < T; tid++) pass_prologue<S>(a, t, tid, T, lds.data());
         for (int k = 0; k < n; k++)  // a barrier separates consecutive steps
             for (uint32_t tid = 0; tid < T; tid++) pass_step<S, KNZ, INV>(k, a, t, tid, T, lds.data());
     }

@@ -52,6 +52,7 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
     const PassTile t = pass_tile(a, bid);
     constexpr int n = pass_steps<S>();
+    pass_prologue<S>(a, t, threadIdx.x, blockDim.x, lds);
     pass_step<S, KNZ, INV>(0, a, t, threadIdx.x, blockDim.x, lds);
     if (n > 1) {
         __syncthreads();
@@ -63,30 +64,46 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
     }
 }
 
+// Launch one instantiation; dynamic LDS above the 64 KB default needs the
+// kernel's limit raised first (gfx950 has 160 KB of LDS per CU).
+template <int S, int KNZ, bool INV>
+hipError_t launch_one(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
+{
+    static size_t raised = 64 * 1024;
+    if (shmem > raised) {
+        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+        if (e != hipSuccess) return e;
+        raised = shmem;
+    }
+    ntt_pass_kernel<S, KNZ, INV><<<grid, kNttThreads, shmem, s>>>(a);
+    return hipGetLastError();
+}
+
 template <int S, bool INV>
-void launch_pass_s(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_pass_s(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
 {
     switch (knz) {
-        case 1: ntt_pass_kernel<S, 1, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
-        case 2: ntt_pass_kernel<S, 2, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
-        case 4: ntt_pass_kernel<S, 4, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
-        default: ntt_pass_kernel<S, 8, INV><<<grid, kNttThreads, shmem, s>>>(a); break;
+        case 1: return launch_one<S, 1, INV>(a, grid, shmem, s);
+        case 2: return launch_one<S, 2, INV>(a, grid, shmem, s);
+        case 4: return launch_one<S, 4, INV>(a, grid, shmem, s);
+        default: return launch_one<S, 8, INV>(a, grid, shmem, s);
     }
 }
 
 template <bool INV>
-void launch_pass(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_pass(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
 {
     switch (a.s) {
-        case 1: launch_pass_s<1, INV>(a, knz, grid, shmem, s); break;
-        case 2: launch_pass_s<2, INV>(a, knz, grid, shmem, s); break;
-        case 3: launch_pass_s<3, INV>(a, knz, grid, shmem, s); break;
-        case 4: launch_pass_s<4, INV>(a, knz, grid, shmem, s); break;
-        case 5: launch_pass_s<5, INV>(a, knz, grid, shmem, s); break;
-        case 6: launch_pass_s<6, INV>(a, knz, grid, shmem, s); break;
-        case 7: launch_pass_s<7, INV>(a, knz, grid, shmem, s); break;
-        case 8: launch_pass_s<8, INV>(a, knz, grid, shmem, s); break;
-        default: launch_pass_s<9, INV>(a, knz, grid, shmem, s); break;
+        case 1: return launch_pass_s<1, INV>(a, knz, grid, shmem, s);
+        case 2: return launch_pass_s<2, INV>(a, knz, grid, shmem, s);
+        case 3: return launch_pass_s<3, INV>(a, knz, grid, shmem, s);
+        case 4: return launch_pass_s<4, INV>(a, knz, grid, shmem, s);
+        case 5: return launch_pass_s<5, INV>(a, knz, grid, shmem, s);
+        case 6: return launch_pass_s<6, INV>(a, knz, grid, shmem, s);
+        case 7: return launch_pass_s<7, INV>(a, knz, grid, shmem, s);
+        case 8: return launch_pass_s<8, INV>(a, knz, grid, shmem, s);
+        default: return launch_pass_s<9, INV>(a, knz, grid, shmem, s);
     }
 }
 
@@ -122,13 +139,11 @@ int run_passes(const Plan& p, uint64_t w, const uint64_t* in, uint64_t in_rows, 
             if ((blocks % gx) != 0) return ZKIE_ERR_INVALID;
             grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
         }
-        ProfMark m = prof_begin(a.last ? "ntt_pass_last" : "ntt_pass", s);
-        if (inverse)
-            launch_pass<true>(a, pass_knz(a), grid, pass_lds_bytes(a), s);
-        else
-            launch_pass<false>(a, pass_knz(a), grid, pass_lds_bytes(a), s);
+        ProfMark m = prof_begin(a.last ? "ntt_pass_last" : (i == 0 ? "ntt_pass_first" : "ntt_pass_mid"), s);
+        const hipError_t e = inverse ? launch_pass<true>(a, pass_knz(a), grid, pass_lds_bytes(a), s)
+                                     : launch_pass<false>(a, pass_knz(a), grid, pass_lds_bytes(a), s);
         prof_end(m, s);
-        ZK_LAUNCHED();
+        ZK_TRY(e);
         B -= a.s;
     }
     return ZKIE_OK;

@@ -222,13 +222,19 @@ __host__ __device__ __forceinline__ uint64_t pass_load_elem(const PassArgs& a, c
 // Global destination of frequency i1, vector lane v (inter-pass twiddle,
 // last-pass scale and canonical form applied here).
 __host__ __device__ __forceinline__ void pass_store_elem(const PassArgs& a, const PassTile& t,
-                                                         uint32_t i1, uint32_t v, uint64_t val)
+                                                         uint32_t i1, uint32_t v, uint64_t val,
+                                                         const uint64_t* twtab)
 {
     const uint64_t c = t.c0 + (v & ((1u << a.logC) - 1));
     if (!a.last) {
         const uint64_t j2 = t.j20 + (v >> a.logC);
-        const uint64_t ex = (uint64_t)i1 * j2;
-        if (ex) val = gl_mul(val, pass_root_pow(a, ex));
+        if (twtab) {
+            ZK_BOUND(i1, 1u << a.s);
+            val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
+        } else {
+            const uint64_t ex = (uint64_t)i1 * j2;
+            if (ex) val = gl_mul(val, pass_root_pow(a, ex));
+        }
         const uint64_t idx = (t.blk + (uint64_t)i1 * t.N2 + j2) * a.w + c;
         ZK_BOUND(idx, a.out_len);
         a.out[idx] = val;
@@ -246,7 +252,7 @@ __host__ __device__ __forceinline__ void pass_store_elem(const PassArgs& a, cons
 // outputs to HBM (last step).
 template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL>
 __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, uint32_t tid,
-                                                  uint32_t T, uint64_t* lds)
+                                                  uint32_t T, uint64_t* lds, const uint64_t* twtab)
 {
     constexpr int R = 1 << RL;
     constexpr int QL = BS - RL;
@@ -282,7 +288,7 @@ __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassT
             const uint32_t f = bit_reverse((uint32_t)idx, RL);
             const uint32_t pos = base + (f << QL);
             if (TO_GLOBAL) {
-                pass_store_elem(a, t, digit_reverse<S>(pos), v, x[idx]);
+                pass_store_elem(a, t, digit_reverse<S>(pos), v, x[idx], twtab);
             } else {
                 ZK_BOUND((pos << logV) | v, (1u << S) << logV);
                 lds[(pos << logV) | v] = x[idx];
@@ -298,6 +304,29 @@ constexpr int pass_steps()
     return Radix<S>::n;
 }
 
+// Whether the pass keeps a table of its inter-pass twiddles in LDS: a
+// multi-step, non-last pass whose tile holds a single j2 (J = 1). Then every
+// output i1 is multiplied by w_N^(i1 j2) with the same j2, and the 2^S powers
+// are formed once per workgroup after the tile (LDS words [2^S V, 2^S V + 2^S)).
+__host__ __device__ __forceinline__ bool pass_uses_twtab(const PassArgs& a)
+{
+    return a.s > 3 && !a.last && a.logJ == 0;
+}
+
+// Before step 0: fill the twiddle table (no barrier needed before step 0;
+// the table is read by the last step, after at least one barrier).
+template <int S>
+__host__ __device__ __forceinline__ void pass_prologue(const PassArgs& a, const PassTile& t,
+                                                       uint32_t tid, uint32_t T, uint64_t* lds)
+{
+    if (!pass_uses_twtab(a)) return;
+    uint64_t* tab = lds + ((1u << S) << t.logV);
+    for (uint32_t i = tid; i < (1u << S); i += T) {
+        const uint64_t ex = (uint64_t)i * t.j20;
+        tab[i] = ex ? pass_root_pow(a, ex) : 1;
+    }
+}
+
 // Step `k` of the S-point sub-DFT (k < pass_steps<S>()). The caller puts a
 // workgroup barrier between consecutive steps.
 template <int S, int KNZ, bool INV>
@@ -306,18 +335,19 @@ __host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, con
 {
     using Rd = Radix<S>;
     constexpr int n = Rd::n;
+    const uint64_t* tab = pass_uses_twtab(a) ? lds + ((1u << S) << t.logV) : nullptr;
     if (k == 0) {
         if (n == 1)
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, true>(a, t, tid, T, lds);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, true>(a, t, tid, T, lds, nullptr);
         else
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, false>(a, t, tid, T, lds);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, false>(a, t, tid, T, lds, nullptr);
     } else if (k == 1) {
         if (n == 2)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true>(a, t, tid, T, lds);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true>(a, t, tid, T, lds, tab);
         else if (n == 3)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false>(a, t, tid, T, lds);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false>(a, t, tid, T, lds, nullptr);
     } else if (k == 2) {
-        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true>(a, t, tid, T, lds);
+        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true>(a, t, tid, T, lds, tab);
     }
 }
 

@@ -112,7 +112,10 @@ inline PassArgs pass_args(const Plan& p, uint32_t i, uint32_t B, uint64_t w, con
 // LDS of a pass: the N1 x V tile, unless the sub-DFT is a single step.
 inline size_t pass_lds_bytes(const PassArgs& a)
 {
-    return a.s <= 3 ? 0 : ((size_t)1 << (a.s + a.logC + a.logJ)) * 8;
+    if (a.s <= 3) return 0;
+    size_t words = (size_t)1 << (a.s + a.logC + a.logJ);
+    if (pass_uses_twtab(a)) words += (size_t)1 << a.s;
+    return words * 8;
 }
 
 // Non-zero inputs among the R = 2^r0 inputs of a step-0 radix DFT: an LDE's
