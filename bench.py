@@ -6,7 +6,7 @@ One step = one commitment of the resident input: coset/subgroup LDE (blowup
 one fold round (k = 4) over the codeword, on 2^24 rows x 16 columns of
 uniform Goldilocks elements (2^28 input elements). Prints one JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N]
                   [--no-cpu-baseline]
 """
 from __future__ import annotations
@@ -31,8 +31,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=1 << 16,
+    ap.add_argument("--cpu-rows", type=int, default=1 << 20,
                     help="coefficient rows of the CPU baseline sample")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the run, copy MIB MiB device to device three times (a plain "
+                         "copy kernel of known size for scaling rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -144,7 +147,7 @@ def main():
         "vs_baseline": None,
         "dtype": "u64",
         "data": "synthetic",
-        "config": {"workload": f"config{wl.number}: {wl.name}", "rows": wl.rows, "cols": wl.cols,
+        "config": {"workload": wl.name, "rows": wl.rows, "cols": wl.cols,
                    "log_blowup": wl.log_blowup, "fold_k": wl.fold_k,
                    "codeword_rows": n, "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "kernel": "p2_leaf", "achieved": achieved,
@@ -156,6 +159,13 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
     print(json.dumps(out), flush=True)
+    if args.copy_calibration:
+        nbytes = args.copy_calibration << 20
+        src, dst = DeviceBuffer(nbytes // 8), DeviceBuffer(nbytes // 8)
+        for _ in range(3):
+            N.check(L.zkie_memcpy_dtod(dst.addr, src.addr, nbytes, None), "copy")
+        N.check(L.zkie_device_synchronize(), "sync")
+        print(f"copy calibration: 3 device-to-device copies of {nbytes} bytes", file=sys.stderr)
 
 
 if __name__ == "__main__":
