@@ -68,9 +68,59 @@ __host__ __device__ __forceinline__ uint64_t gl_reduce128(uint64_t lo, uint64_t 
     return r;
 }
 
+#ifndef ZK_MUL_ASM
+#define ZK_MUL_ASM 1
+#endif
+
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+// a * b mod p in 15 VALU instructions on gfx950, using the carry-out of
+// v_mad_u64_u32, which the compiler does not use on its own:
+//   P = a0 b0,  T = a0 b1 + P.hi,  U + c 2^64 = a1 b0 + T  (carry c kept as a lane mask),
+//   H = a1 b1 + U.hi,  L = U.lo 2^32 + P.lo,
+//   a b = L + 2^64 H + 2^96 c = L + eps H.lo - H.hi - c   (2^64 = eps, 2^96 = -1).
+// S = L + eps H.lo wraps at most once (carry folds back as + eps, no second
+// wrap); S - H.hi - c borrows at most once (borrow folds back as - eps on a
+// value >= 2^64 - 2^32, no second borrow). A VALU write of an SGPR needs two
+// wait states before a VALU reads it as carry-in or lane mask (s_nop 1).
+__device__ __forceinline__ uint64_t gl_mul_dev(uint64_t a, uint64_t b)
+{
+    const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
+    const uint32_t b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+    const uint64_t P = (uint64_t)a0 * b0;
+    const uint64_t T = (uint64_t)a0 * b1 + (P >> 32);
+    uint64_t U, m;
+    asm("v_mad_u64_u32 %0, %1, %2, %3, %4" : "=&v"(U), "=s"(m) : "v"(a1), "v"(b0), "v"(T));
+    const uint64_t H = (uint64_t)a1 * b1 + (U >> 32);
+    const uint64_t L = (U << 32) | (uint32_t)P;
+    uint64_t S, m1;
+    uint32_t c1;
+    asm("v_mad_u64_u32 %0, %1, %3, -1, %4\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, 1, %1\n\t"
+        "v_mad_u64_u32 %0, %1, %2, -1, %0"
+        : "=&v"(S), "=&s"(m1), "=&v"(c1)
+        : "v"((uint32_t)H), "v"(L));
+    uint32_t d0, d1, e;
+    uint64_t k;
+    asm("v_subb_co_u32_e64 %0, %3, %4, %6, %7\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %5, 0, %3\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
+        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %1, 0, %3"
+        : "=&v"(d0), "=&v"(d1), "=&v"(e), "=&s"(k)
+        : "v"((uint32_t)S), "v"((uint32_t)(S >> 32)), "v"((uint32_t)(H >> 32)), "s"(m));
+    return ((uint64_t)d1 << 32) | d0;
+}
+#endif
+
 __host__ __device__ __forceinline__ uint64_t gl_mul(uint64_t a, uint64_t b)
 {
-#if defined(__HIP_DEVICE_COMPILE__) || defined(ZK_LIMB_MUL_ON_HOST)
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    return gl_mul_dev(a, b);
+#elif defined(__HIP_DEVICE_COMPILE__) || defined(ZK_LIMB_MUL_ON_HOST)
     const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
     const uint32_t b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
     const uint64_t p00 = (uint64_t)a0 * b0;
@@ -87,7 +137,9 @@ __host__ __device__ __forceinline__ uint64_t gl_mul(uint64_t a, uint64_t b)
 
 __host__ __device__ __forceinline__ uint64_t gl_sqr(uint64_t a)
 {
-#if defined(__HIP_DEVICE_COMPILE__) || defined(ZK_LIMB_MUL_ON_HOST)
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    return gl_mul_dev(a, a);
+#elif defined(__HIP_DEVICE_COMPILE__) || defined(ZK_LIMB_MUL_ON_HOST)
     const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
     const uint64_t p00 = (uint64_t)a0 * a0;
     const uint64_t c = (uint64_t)a0 * a1;  // cross term, counted twice
