@@ -153,6 +153,60 @@ __host__ __device__ __forceinline__ uint64_t gl_sqr(uint64_t a)
 #endif
 }
 
+// Two independent products (x = a b, y = c d) with the steps of gl_mul_dev
+// interleaved, so that each product's instructions fill the other's SGPR
+// wait states instead of s_nop cycles.
+__host__ __device__ __forceinline__ void gl_mul2(uint64_t a, uint64_t b, uint64_t c, uint64_t d,
+                                                 uint64_t& x, uint64_t& y)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32), b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+    const uint32_t c0 = (uint32_t)c, c1 = (uint32_t)(c >> 32), d0 = (uint32_t)d, d1 = (uint32_t)(d >> 32);
+    const uint64_t Pa = (uint64_t)a0 * b0, Pb = (uint64_t)c0 * d0;
+    const uint64_t Ta = (uint64_t)a0 * b1 + (Pa >> 32), Tb = (uint64_t)c0 * d1 + (Pb >> 32);
+    uint64_t Ua, Ub, ma, mb;
+    asm("v_mad_u64_u32 %0, %2, %4, %5, %6\n\t"
+        "v_mad_u64_u32 %1, %3, %7, %8, %9"
+        : "=&v"(Ua), "=&v"(Ub), "=&s"(ma), "=&s"(mb)
+        : "v"(a1), "v"(b0), "v"(Ta), "v"(c1), "v"(d0), "v"(Tb));
+    const uint64_t Ha = (uint64_t)a1 * b1 + (Ua >> 32), Hb = (uint64_t)c1 * d1 + (Ub >> 32);
+    const uint64_t La = (Ua << 32) | (uint32_t)Pa, Lb = (Ub << 32) | (uint32_t)Pb;
+    uint64_t Sa, Sb, ka, kb;
+    uint32_t ca, cb;
+    asm("v_mad_u64_u32 %0, %2, %6, -1, %7\n\t"
+        "v_mad_u64_u32 %1, %3, %8, -1, %9\n\t"
+        "s_nop 0\n\t"
+        "v_cndmask_b32_e64 %4, 0, 1, %2\n\t"
+        "v_cndmask_b32_e64 %5, 0, 1, %3\n\t"
+        "v_mad_u64_u32 %0, %2, %4, -1, %0\n\t"
+        "v_mad_u64_u32 %1, %3, %5, -1, %1"
+        : "=&v"(Sa), "=&v"(Sb), "=&s"(ka), "=&s"(kb), "=&v"(ca), "=&v"(cb)
+        : "v"((uint32_t)Ha), "v"(La), "v"((uint32_t)Hb), "v"(Lb));
+    uint32_t xa0, xa1, xb0, xb1, ea, eb;
+    asm("v_subb_co_u32_e64 %0, %6, %8, %10, %11\n\t"
+        "v_subb_co_u32_e64 %2, %7, %12, %14, %15\n\t"
+        "s_nop 0\n\t"
+        "v_subb_co_u32_e64 %1, %6, %9, 0, %6\n\t"
+        "v_subb_co_u32_e64 %3, %7, %13, 0, %7\n\t"
+        "s_nop 0\n\t"
+        "v_cndmask_b32_e64 %4, 0, -1, %6\n\t"
+        "v_cndmask_b32_e64 %5, 0, -1, %7\n\t"
+        "v_sub_co_u32_e64 %0, %6, %0, %4\n\t"
+        "v_sub_co_u32_e64 %2, %7, %2, %5\n\t"
+        "s_nop 0\n\t"
+        "v_subb_co_u32_e64 %1, %6, %1, 0, %6\n\t"
+        "v_subb_co_u32_e64 %3, %7, %3, 0, %7"
+        : "=&v"(xa0), "=&v"(xa1), "=&v"(xb0), "=&v"(xb1), "=&v"(ea), "=&v"(eb), "=&s"(ka), "=&s"(kb)
+        : "v"((uint32_t)Sa), "v"((uint32_t)(Sa >> 32)), "v"((uint32_t)(Ha >> 32)), "s"(ma),
+          "v"((uint32_t)Sb), "v"((uint32_t)(Sb >> 32)), "v"((uint32_t)(Hb >> 32)), "s"(mb));
+    x = ((uint64_t)xa1 << 32) | xa0;
+    y = ((uint64_t)xb1 << 32) | xb0;
+#else
+    x = gl_mul(a, b);
+    y = gl_mul(c, d);
+#endif
+}
+
 // x * 2^-k for 1 <= k <= 32, any x < 2^64:
 // x = q 2^k + r, r 2^-k = -r 2^(96-k) = -(m * eps) with m = r 2^(32-k) < 2^32,
 // and -(m * eps) = p - m 2^32 + m = (2^32 - 1 - m) 2^32 + (m + 1).

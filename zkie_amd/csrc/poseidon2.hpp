@@ -37,9 +37,19 @@ struct P2Consts {
 __host__ __device__ __forceinline__ uint64_t sbox7(uint64_t x)
 {
     const uint64_t x2 = gl_sqr(x);
-    const uint64_t x3 = gl_mul(x2, x);
-    const uint64_t x4 = gl_sqr(x2);
+    uint64_t x3, x4;
+    gl_mul2(x2, x, x2, x2, x3, x4);
     return gl_mul(x3, x4);
+}
+
+// x^7 and y^7, the two addition chains interleaved product by product.
+__host__ __device__ __forceinline__ void sbox7_2(uint64_t& x, uint64_t& y)
+{
+    uint64_t x2, y2, x3, y3, x4, y4;
+    gl_mul2(x, x, y, y, x2, y2);
+    gl_mul2(x2, x, y2, y, x3, y3);
+    gl_mul2(x2, x2, y2, y2, x4, y4);
+    gl_mul2(x3, x4, y3, y4, x, y);
 }
 
 // mat4 = [2 3 1 1; 1 2 3 1; 1 1 2 3; 3 1 1 2] on lazy sums
@@ -127,7 +137,7 @@ __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts
 #pragma unroll 1
     for (int r = 0; r < 8; r++) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) st[i] = sbox7(st[i]);
+        for (int i = 0; i < 16; i += 2) sbox7_2(st[i], st[i + 1]);
         if (r == 3) {
             mds_light16<false>(st, nullptr);
 #pragma unroll 1
