@@ -16,7 +16,7 @@ using namespace zk;
 
 namespace {
 
-template <int S, int KNZ, bool INV>
+template <int S, int KNZ, bool INV, int ROLE>
 void run_pass_t(const PassArgs& a, uint32_t T)
 {
     const uint64_t blocks = pass_blocks(a);
@@ -24,20 +24,31 @@ void run_pass_t(const PassArgs& a, uint32_t T)
     constexpr int n = pass_steps<S>();
     for (uint64_t bid = 0; bid < blocks; bid++) {
         const PassTile t = pass_tile(a, bid);
-        for (uint32_t tid = 0; tid < T; tid++) pass_prologue<S>(a, t, tid, T, lds.data());
+        for (uint32_t tid = 0; tid < T; tid++) pass_prologue<S, ROLE>(a, t, tid, T, lds.data());
         for (int k = 0; k < n; k++)  // a barrier separates consecutive steps
-            for (uint32_t tid = 0; tid < T; tid++) pass_step<S, KNZ, INV>(k, a, t, tid, T, lds.data());
+            for (uint32_t tid = 0; tid < T; tid++) pass_step<S, KNZ, INV, ROLE>(k, a, t, tid, T, lds.data());
+    }
+}
+
+template <int S, bool INV, int ROLE>
+void run_pass_r(const PassArgs& a, int knz, uint32_t T)
+{
+    switch (knz) {
+        case 1: run_pass_t<S, 1, INV, ROLE>(a, T); break;
+        case 2: run_pass_t<S, 2, INV, ROLE>(a, T); break;
+        case 4: run_pass_t<S, 4, INV, ROLE>(a, T); break;
+        default: run_pass_t<S, 8, INV, ROLE>(a, T); break;
     }
 }
 
 template <int S, bool INV>
 void run_pass_s(const PassArgs& a, int knz, uint32_t T)
 {
-    switch (knz) {
-        case 1: run_pass_t<S, 1, INV>(a, T); break;
-        case 2: run_pass_t<S, 2, INV>(a, T); break;
-        case 4: run_pass_t<S, 4, INV>(a, T); break;
-        default: run_pass_t<S, 8, INV>(a, T); break;
+    switch (pass_role(a)) {
+        case kRoleTwiddle: run_pass_r<S, INV, kRoleTwiddle>(a, knz, T); break;
+        case kRoleTable: run_pass_r<S, INV, kRoleTable>(a, knz, T); break;
+        case kRoleLast: run_pass_r<S, INV, kRoleLast>(a, knz, T); break;
+        default: run_pass_r<S, INV, kRoleLastScale>(a, knz, T); break;
     }
 }
 

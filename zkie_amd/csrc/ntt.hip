@@ -45,49 +45,70 @@ int ensure_tables(const uint64_t** out)
     return ZKIE_OK;
 }
 
-template <int S, int KNZ, bool INV>
+template <int S, int KNZ, bool INV, int ROLE>
 __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 {
     extern __shared__ uint64_t lds[];
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
     const PassTile t = pass_tile(a, bid);
     constexpr int n = pass_steps<S>();
-    pass_prologue<S>(a, t, threadIdx.x, blockDim.x, lds);
-    pass_step<S, KNZ, INV>(0, a, t, threadIdx.x, blockDim.x, lds);
+    pass_prologue<S, ROLE>(a, t, threadIdx.x, blockDim.x, lds);
+    pass_step<S, KNZ, INV, ROLE>(0, a, t, threadIdx.x, blockDim.x, lds);
     if (n > 1) {
         __syncthreads();
-        pass_step<S, KNZ, INV>(1, a, t, threadIdx.x, blockDim.x, lds);
+        pass_step<S, KNZ, INV, ROLE>(1, a, t, threadIdx.x, blockDim.x, lds);
     }
     if (n > 2) {
         __syncthreads();
-        pass_step<S, KNZ, INV>(2, a, t, threadIdx.x, blockDim.x, lds);
+        pass_step<S, KNZ, INV, ROLE>(2, a, t, threadIdx.x, blockDim.x, lds);
     }
 }
 
 // Launch one instantiation; dynamic LDS above the 64 KB default needs the
 // kernel's limit raised first (gfx950 has 160 KB of LDS per CU).
-template <int S, int KNZ, bool INV>
+template <int S, int KNZ, bool INV, int ROLE>
 hipError_t launch_one(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
 {
     static size_t raised = 64 * 1024;
     if (shmem > raised) {
-        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV>,
+        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
         if (e != hipSuccess) return e;
         raised = shmem;
     }
-    ntt_pass_kernel<S, KNZ, INV><<<grid, kNttThreads, shmem, s>>>(a);
+    ntt_pass_kernel<S, KNZ, INV, ROLE><<<grid, kNttThreads, shmem, s>>>(a);
     return hipGetLastError();
+}
+
+// Instances: forward passes prune zero inputs of an LDE (KNZ < 8) and never
+// scale; inverse passes read full inputs and scale in the last pass.
+template <int S, bool INV, int ROLE>
+hipError_t launch_pass_r(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+{
+    if (INV) return launch_one<S, 8, INV, ROLE>(a, grid, shmem, s);
+    switch (knz) {
+        case 1: return launch_one<S, 1, INV, ROLE>(a, grid, shmem, s);
+        case 2: return launch_one<S, 2, INV, ROLE>(a, grid, shmem, s);
+        case 4: return launch_one<S, 4, INV, ROLE>(a, grid, shmem, s);
+        default: return launch_one<S, 8, INV, ROLE>(a, grid, shmem, s);
+    }
 }
 
 template <int S, bool INV>
 hipError_t launch_pass_s(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
 {
-    switch (knz) {
-        case 1: return launch_one<S, 1, INV>(a, grid, shmem, s);
-        case 2: return launch_one<S, 2, INV>(a, grid, shmem, s);
-        case 4: return launch_one<S, 4, INV>(a, grid, shmem, s);
-        default: return launch_one<S, 8, INV>(a, grid, shmem, s);
+    switch (pass_role(a)) {
+        case kRoleTwiddle: return launch_pass_r<S, INV, kRoleTwiddle>(a, knz, grid, shmem, s);
+        case kRoleTable: return launch_pass_r<S, INV, kRoleTable>(a, knz, grid, shmem, s);
+        default:
+            // A forward last pass never scales and an inverse one always does (1/n, n > 1).
+            if constexpr (INV) {
+                if (pass_role(a) != kRoleLastScale) return hipErrorInvalidValue;
+                return launch_pass_r<S, INV, kRoleLastScale>(a, knz, grid, shmem, s);
+            } else {
+                if (pass_role(a) != kRoleLast) return hipErrorInvalidValue;
+                return launch_pass_r<S, INV, kRoleLast>(a, knz, grid, shmem, s);
+            }
     }
 }
 

@@ -66,8 +66,17 @@ struct PassTile {
     uint64_t c0;   // first column
     uint64_t j20;  // first j2
     uint64_t N2;
+    uint64_t nat0;  // last pass: natural row of blk (frequency i1 adds i1 2^(L - s))
     uint32_t logV;
 };
+
+// What the last step of a pass does with each output (a compile-time choice,
+// so that a pass carries no per-element branches):
+//   kRoleTwiddle  non-last pass, w_N^(i1 j2) formed from the two-level table;
+//   kRoleTable    non-last pass with one j2 per tile, w_N^(i1 j2) from LDS;
+//   kRoleLast     last pass, natural row order, canonical output;
+//   kRoleLastScale  the same, times the pass scale (1/n of an inverse DFT).
+enum PassRole { kRoleTwiddle = 0, kRoleTable = 1, kRoleLast = 2, kRoleLastScale = 3 };
 
 __host__ __device__ __forceinline__ uint32_t bit_reverse(uint32_t x, uint32_t bits)
 {
@@ -78,6 +87,21 @@ __host__ __device__ __forceinline__ uint64_t pass_blocks(const PassArgs& a)
 {
     const uint32_t logN2 = a.B - a.s;
     return ((1ull << a.L) >> a.B) * ((1ull << logN2) >> a.logJ) * (a.w >> a.logC);
+}
+
+// Natural row of position pos after all passes: the digit of pass p (its
+// s_p bits, taken from the top of pos) lands at bit s_0 + ... + s_(p-1).
+__host__ __device__ __forceinline__ uint64_t pass_natural_row(const PassArgs& a, uint64_t pos)
+{
+    uint64_t nat = 0;
+    uint32_t rem = a.L, shift_nat = 0;
+    for (uint32_t p = 0; p < a.np; p++) {
+        const uint32_t sp = a.sb[p];
+        rem -= sp;
+        nat |= ((pos >> rem) & ((1ull << sp) - 1)) << shift_nat;
+        shift_nat += sp;
+    }
+    return nat;
 }
 
 __host__ __device__ __forceinline__ PassTile pass_tile(const PassArgs& a, uint64_t bid)
@@ -94,6 +118,7 @@ __host__ __device__ __forceinline__ PassTile pass_tile(const PassArgs& a, uint64
     t.c0 = ct << a.logC;
     t.j20 = jt << a.logJ;
     t.logV = a.logC + a.logJ;
+    t.nat0 = a.last ? pass_natural_row(a, t.blk) : 0;
     return t;
 }
 
@@ -102,19 +127,6 @@ __host__ __device__ __forceinline__ uint64_t pass_root_pow(const PassArgs& a, ui
 {
     const uint64_t E = e << (32 - a.B);
     return gl_mul(a.twlo[E & 0xFFFF], a.twhi[E >> 16]);
-}
-
-__host__ __device__ __forceinline__ uint64_t pass_natural_row(const PassArgs& a, uint64_t pos)
-{
-    uint64_t nat = 0;
-    uint32_t rem = a.L, shift_nat = 0;
-    for (uint32_t p = 0; p < a.np; p++) {
-        const uint32_t sp = a.sb[p];
-        rem -= sp;
-        nat |= ((pos >> rem) & ((1ull << sp) - 1)) << shift_nat;
-        shift_nat += sp;
-    }
-    return nat;
 }
 
 // Radix decomposition of an S-point sub-DFT: digits r_0, r_1, r_2 (bits).
@@ -220,37 +232,36 @@ __host__ __device__ __forceinline__ uint64_t pass_load_elem(const PassArgs& a, c
 }
 
 // Global destination of frequency i1, vector lane v (inter-pass twiddle,
-// last-pass scale and canonical form applied here).
-__host__ __device__ __forceinline__ void pass_store_elem(const PassArgs& a, const PassTile& t,
-                                                         uint32_t i1, uint32_t v, uint64_t val,
-                                                         const uint64_t* twtab)
+// last-pass scale and canonical form applied here). `row0` is the row of
+// frequency 0 for this lane (the natural row of the tile's first row in the
+// last pass); frequency i1 lies `i1 * rstride` rows further.
+template <int ROLE>
+__host__ __device__ __forceinline__ void pass_store_elem(const PassArgs& a, uint32_t i1, uint32_t v,
+                                                         uint64_t val, const uint64_t* twtab,
+                                                         uint64_t row0, uint64_t rstride, uint64_t c,
+                                                         uint64_t j2)
 {
-    const uint64_t c = t.c0 + (v & ((1u << a.logC) - 1));
-    if (!a.last) {
-        const uint64_t j2 = t.j20 + (v >> a.logC);
-        if (twtab) {
-            ZK_BOUND(i1, 1u << a.s);
-            val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
-        } else {
-            const uint64_t ex = (uint64_t)i1 * j2;
-            if (ex) val = gl_mul(val, pass_root_pow(a, ex));
-        }
-        const uint64_t idx = (t.blk + (uint64_t)i1 * t.N2 + j2) * a.w + c;
-        ZK_BOUND(idx, a.out_len);
-        a.out[idx] = val;
+    if (ROLE == kRoleTable) {
+        ZK_BOUND(i1, 1u << a.s);
+        val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
+    } else if (ROLE == kRoleTwiddle) {
+        const uint64_t ex = (uint64_t)i1 * j2;
+        if (ex) val = gl_mul(val, pass_root_pow(a, ex));
     } else {
-        if (a.scale != 1) val = gl_mul(val, a.scale);
-        const uint64_t idx = pass_natural_row(a, t.blk + i1) * a.w + c;
-        ZK_BOUND(idx, a.out_len);
-        a.out[idx] = gl_canon(val);
+        if (ROLE == kRoleLastScale) val = gl_mul(val, a.scale);
+        val = gl_canon(val);
     }
+    const uint64_t idx = (row0 + (uint64_t)i1 * rstride) * a.w + c;
+    ZK_BOUND(idx, a.out_len);
+    a.out[idx] = val;
+    (void)v;
 }
 
 // One radix-2^RL DIF step on sub-problems of 2^BS points of an S-point DFT.
 // FROM_GLOBAL: inputs from HBM (step 0; only the first KNZ of the R inputs
 // can be non-zero, the rest are the zero padding of an LDE). TO_GLOBAL:
 // outputs to HBM (last step).
-template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL>
+template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE>
 __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, uint32_t tid,
                                                   uint32_t T, uint64_t* lds, const uint64_t* twtab)
 {
@@ -288,7 +299,14 @@ __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassT
             const uint32_t f = bit_reverse((uint32_t)idx, RL);
             const uint32_t pos = base + (f << QL);
             if (TO_GLOBAL) {
-                pass_store_elem(a, t, digit_reverse<S>(pos), v, x[idx], twtab);
+                const uint64_t c = t.c0 + (v & ((1u << a.logC) - 1));
+                const uint64_t j2 = t.j20 + (v >> a.logC);
+                if (ROLE >= kRoleLast)
+                    pass_store_elem<ROLE>(a, digit_reverse<S>(pos), v, x[idx], twtab, t.nat0,
+                                          1ull << (a.L - a.s), c, 0);
+                else
+                    pass_store_elem<ROLE>(a, digit_reverse<S>(pos), v, x[idx], twtab, t.blk + j2,
+                                          t.N2, c, j2);
             } else {
                 ZK_BOUND((pos << logV) | v, (1u << S) << logV);
                 lds[(pos << logV) | v] = x[idx];
@@ -315,11 +333,11 @@ __host__ __device__ __forceinline__ bool pass_uses_twtab(const PassArgs& a)
 
 // Before step 0: fill the twiddle table (no barrier needed before step 0;
 // the table is read by the last step, after at least one barrier).
-template <int S>
+template <int S, int ROLE>
 __host__ __device__ __forceinline__ void pass_prologue(const PassArgs& a, const PassTile& t,
                                                        uint32_t tid, uint32_t T, uint64_t* lds)
 {
-    if (!pass_uses_twtab(a)) return;
+    if (ROLE != kRoleTable) return;
     uint64_t* tab = lds + ((1u << S) << t.logV);
     for (uint32_t i = tid; i < (1u << S); i += T) {
         const uint64_t ex = (uint64_t)i * t.j20;
@@ -329,26 +347,33 @@ __host__ __device__ __forceinline__ void pass_prologue(const PassArgs& a, const 
 
 // Step `k` of the S-point sub-DFT (k < pass_steps<S>()). The caller puts a
 // workgroup barrier between consecutive steps.
-template <int S, int KNZ, bool INV>
+template <int S, int KNZ, bool INV, int ROLE>
 __host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, const PassTile& t,
                                                    uint32_t tid, uint32_t T, uint64_t* lds)
 {
     using Rd = Radix<S>;
     constexpr int n = Rd::n;
-    const uint64_t* tab = pass_uses_twtab(a) ? lds + ((1u << S) << t.logV) : nullptr;
+    const uint64_t* tab = ROLE == kRoleTable ? lds + ((1u << S) << t.logV) : nullptr;
     if (k == 0) {
         if (n == 1)
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, true>(a, t, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, true, ROLE>(a, t, tid, T, lds, nullptr);
         else
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, false>(a, t, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, false, ROLE>(a, t, tid, T, lds, nullptr);
     } else if (k == 1) {
         if (n == 2)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true>(a, t, tid, T, lds, tab);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE>(a, t, tid, T, lds, tab);
         else if (n == 3)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false>(a, t, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false, ROLE>(a, t, tid, T, lds, nullptr);
     } else if (k == 2) {
-        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true>(a, t, tid, T, lds, tab);
+        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE>(a, t, tid, T, lds, tab);
     }
+}
+
+// Role of a pass (see PassRole).
+__host__ __device__ __forceinline__ int pass_role(const PassArgs& a)
+{
+    if (a.last) return a.scale != 1 ? kRoleLastScale : kRoleLast;
+    return pass_uses_twtab(a) ? kRoleTable : kRoleTwiddle;
 }
 
 }  // namespace zk
