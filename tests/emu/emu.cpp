@@ -6,6 +6,7 @@
 // phase for every thread of every workgroup, in the order the barriers
 // impose, so index mistakes abort here instead of faulting a GPU.
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -16,28 +17,41 @@ using namespace zk;
 
 namespace {
 
-template <int S, int KNZ, bool INV, int ROLE>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV>
 void run_pass_t(const PassArgs& a, uint32_t T)
 {
     const uint64_t blocks = pass_blocks(a);
     std::vector<uint64_t> lds(pass_lds_bytes(a) / 8 + 1);
     constexpr int n = pass_steps<S>();
+    if (T % (1u << (a.logC + a.logJ)) != 0) std::abort();  // a thread keeps one vector lane
     for (uint64_t bid = 0; bid < blocks; bid++) {
         const PassTile t = pass_tile(a, bid);
         for (uint32_t tid = 0; tid < T; tid++) pass_prologue<S, ROLE>(a, t, tid, T, lds.data());
         for (int k = 0; k < n; k++)  // a barrier separates consecutive steps
-            for (uint32_t tid = 0; tid < T; tid++) pass_step<S, KNZ, INV, ROLE>(k, a, t, tid, T, lds.data());
+            for (uint32_t tid = 0; tid < T; tid++) {
+                const PassLane l = pass_lane(a, t, tid);
+                pass_step<S, KNZ, INV, ROLE, LOGV>(k, a, t, l, tid, T, lds.data());
+            }
     }
+}
+
+template <int S, int KNZ, bool INV, int ROLE>
+void run_pass_v(const PassArgs& a, uint32_t T)
+{
+    if (a.logC + a.logJ == 4)
+        run_pass_t<S, KNZ, INV, ROLE, 4>(a, T);
+    else
+        run_pass_t<S, KNZ, INV, ROLE, -1>(a, T);
 }
 
 template <int S, bool INV, int ROLE>
 void run_pass_r(const PassArgs& a, int knz, uint32_t T)
 {
     switch (knz) {
-        case 1: run_pass_t<S, 1, INV, ROLE>(a, T); break;
-        case 2: run_pass_t<S, 2, INV, ROLE>(a, T); break;
-        case 4: run_pass_t<S, 4, INV, ROLE>(a, T); break;
-        default: run_pass_t<S, 8, INV, ROLE>(a, T); break;
+        case 1: run_pass_v<S, 1, INV, ROLE>(a, T); break;
+        case 2: run_pass_v<S, 2, INV, ROLE>(a, T); break;
+        case 4: run_pass_v<S, 4, INV, ROLE>(a, T); break;
+        default: run_pass_v<S, 8, INV, ROLE>(a, T); break;
     }
 }
 

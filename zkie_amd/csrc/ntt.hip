@@ -45,39 +45,48 @@ int ensure_tables(const uint64_t** out)
     return ZKIE_OK;
 }
 
-template <int S, int KNZ, bool INV, int ROLE>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV>
 __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 {
     extern __shared__ uint64_t lds[];
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
     const PassTile t = pass_tile(a, bid);
+    const PassLane l = pass_lane(a, t, threadIdx.x);
     constexpr int n = pass_steps<S>();
     pass_prologue<S, ROLE>(a, t, threadIdx.x, blockDim.x, lds);
-    pass_step<S, KNZ, INV, ROLE>(0, a, t, threadIdx.x, blockDim.x, lds);
+    pass_step<S, KNZ, INV, ROLE, LOGV>(0, a, t, l, threadIdx.x, blockDim.x, lds);
     if (n > 1) {
         __syncthreads();
-        pass_step<S, KNZ, INV, ROLE>(1, a, t, threadIdx.x, blockDim.x, lds);
+        pass_step<S, KNZ, INV, ROLE, LOGV>(1, a, t, l, threadIdx.x, blockDim.x, lds);
     }
     if (n > 2) {
         __syncthreads();
-        pass_step<S, KNZ, INV, ROLE>(2, a, t, threadIdx.x, blockDim.x, lds);
+        pass_step<S, KNZ, INV, ROLE, LOGV>(2, a, t, l, threadIdx.x, blockDim.x, lds);
     }
 }
 
 // Launch one instantiation; dynamic LDS above the 64 KB default needs the
 // kernel's limit raised first (gfx950 has 160 KB of LDS per CU).
-template <int S, int KNZ, bool INV, int ROLE>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV>
 hipError_t launch_one(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
 {
     static size_t raised = 64 * 1024;
     if (shmem > raised) {
-        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE>,
+        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
         if (e != hipSuccess) return e;
         raised = shmem;
     }
-    ntt_pass_kernel<S, KNZ, INV, ROLE><<<grid, kNttThreads, shmem, s>>>(a);
+    ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV><<<grid, kNttThreads, shmem, s>>>(a);
     return hipGetLastError();
+}
+
+// Tiles of 16 vector lanes (the usual case) address LDS with immediate offsets.
+template <int S, int KNZ, bool INV, int ROLE>
+hipError_t launch_v(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
+{
+    if (a.logC + a.logJ == 4) return launch_one<S, KNZ, INV, ROLE, 4>(a, grid, shmem, s);
+    return launch_one<S, KNZ, INV, ROLE, -1>(a, grid, shmem, s);
 }
 
 // Instances: forward passes prune zero inputs of an LDE (KNZ < 8) and never
@@ -85,12 +94,12 @@ hipError_t launch_one(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
 template <int S, bool INV, int ROLE>
 hipError_t launch_pass_r(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
 {
-    if (INV) return launch_one<S, 8, INV, ROLE>(a, grid, shmem, s);
+    if (INV) return launch_v<S, 8, INV, ROLE>(a, grid, shmem, s);
     switch (knz) {
-        case 1: return launch_one<S, 1, INV, ROLE>(a, grid, shmem, s);
-        case 2: return launch_one<S, 2, INV, ROLE>(a, grid, shmem, s);
-        case 4: return launch_one<S, 4, INV, ROLE>(a, grid, shmem, s);
-        default: return launch_one<S, 8, INV, ROLE>(a, grid, shmem, s);
+        case 1: return launch_v<S, 1, INV, ROLE>(a, grid, shmem, s);
+        case 2: return launch_v<S, 2, INV, ROLE>(a, grid, shmem, s);
+        case 4: return launch_v<S, 4, INV, ROLE>(a, grid, shmem, s);
+        default: return launch_v<S, 8, INV, ROLE>(a, grid, shmem, s);
     }
 }
 
@@ -175,6 +184,7 @@ int dft_inplace(uint64_t* d_mat, uint64_t* d_tmp, uint32_t lg, uint64_t w, bool 
     if (lg > 32 || (w > 0 && !d_mat)) return ZKIE_ERR_INVALID;
     if (lg == 0 || w == 0) return ZKIE_OK;
     const Plan p = make_plan(lg, w);
+    if (!plan_fits(p, w)) return ZKIE_ERR_INVALID;
     const uint64_t n = 1ull << lg;
     if (p.np == 1) return run_passes(p, w, d_mat, n, nullptr, d_mat, inverse, s);
     if (!d_tmp) {
@@ -224,6 +234,7 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
         src = d_out;
     }
     const Plan p = make_plan(L, w);
+    if (!plan_fits(p, w)) return ZKIE_ERR_INVALID;
     if (p.np == 1) {
         if (src == d_out) {
             // in place, single pass: rows >= h are treated as zero

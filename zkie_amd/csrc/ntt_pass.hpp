@@ -59,6 +59,9 @@ struct PassArgs {
     uint32_t last;
     uint32_t np;
     uint32_t sb[8];
+    uint32_t check_rows;  // step 0 may read rows >= in_rows (read as zero)
+    uint32_t in_stride;   // elements between points j1 and j1 + 1 of a tile (N2 w)
+    uint32_t out_stride;  // elements between frequencies i1 and i1 + 1 (N2 w, last pass 2^(L-s) w)
 };
 
 struct PassTile {
@@ -220,96 +223,136 @@ __host__ __device__ __forceinline__ void dft_small(uint64_t* x)
     }
 }
 
-// Global source element j1 (within the block), vector lane v.
-__host__ __device__ __forceinline__ uint64_t pass_load_elem(const PassArgs& a, const PassTile& t,
-                                                            uint32_t j1, uint32_t v)
-{
-    const uint64_t row = t.blk + (uint64_t)j1 * t.N2 + t.j20 + (v >> a.logC);
-    if (row >= a.in_rows) return 0;
-    const uint64_t idx = row * a.w + t.c0 + (v & ((1u << a.logC) - 1));
-    ZK_BOUND(idx, a.in_len);
-    return a.in[idx];
-}
+// Per-thread addressing of a pass, fixed for all its items: a thread always
+// serves the same vector lane v (the thread count is a multiple of V), so the
+// element index of point j1 is in_base + j1 in_stride and that of frequency i1
+// is out_base + i1 out_stride.
+struct PassLane {
+    uint32_t v;
+    uint64_t in_base, out_base;
+    uint32_t pos_lim;  // step 0: points j1 >= pos_lim lie beyond in_rows
+    uint64_t j2;
+};
 
-// Global destination of frequency i1, vector lane v (inter-pass twiddle,
-// last-pass scale and canonical form applied here). `row0` is the row of
-// frequency 0 for this lane (the natural row of the tile's first row in the
-// last pass); frequency i1 lies `i1 * rstride` rows further.
-template <int ROLE>
-__host__ __device__ __forceinline__ void pass_store_elem(const PassArgs& a, uint32_t i1, uint32_t v,
-                                                         uint64_t val, const uint64_t* twtab,
-                                                         uint64_t row0, uint64_t rstride, uint64_t c,
-                                                         uint64_t j2)
+__host__ __device__ __forceinline__ PassLane pass_lane(const PassArgs& a, const PassTile& t, uint32_t tid)
 {
-    if (ROLE == kRoleTable) {
-        ZK_BOUND(i1, 1u << a.s);
-        val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
-    } else if (ROLE == kRoleTwiddle) {
-        const uint64_t ex = (uint64_t)i1 * j2;
-        if (ex) val = gl_mul(val, pass_root_pow(a, ex));
-    } else {
-        if (ROLE == kRoleLastScale) val = gl_mul(val, a.scale);
-        val = gl_canon(val);
+    PassLane l;
+    l.v = tid & ((1u << t.logV) - 1);
+    const uint64_t c = t.c0 + (l.v & ((1u << a.logC) - 1));
+    l.j2 = t.j20 + (l.v >> a.logC);
+    const uint64_t row0 = t.blk + l.j2;  // row of point 0
+    l.in_base = row0 * a.w + c;
+    l.out_base = (a.last ? t.nat0 : row0) * a.w + c;
+    const uint32_t logN2 = a.B - a.s;
+    if (row0 >= a.in_rows)
+        l.pos_lim = 0;
+    else {
+        const uint64_t lim = ((a.in_rows - row0) + t.N2 - 1) >> logN2;
+        l.pos_lim = lim > (1ull << a.s) ? (1u << a.s) : (uint32_t)lim;
     }
-    const uint64_t idx = (row0 + (uint64_t)i1 * rstride) * a.w + c;
-    ZK_BOUND(idx, a.out_len);
-    a.out[idx] = val;
-    (void)v;
+    return l;
 }
 
 // One radix-2^RL DIF step on sub-problems of 2^BS points of an S-point DFT.
 // FROM_GLOBAL: inputs from HBM (step 0; only the first KNZ of the R inputs
 // can be non-zero, the rest are the zero padding of an LDE). TO_GLOBAL:
-// outputs to HBM (last step).
-template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE>
-__host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, uint32_t tid,
-                                                  uint32_t T, uint64_t* lds, const uint64_t* twtab)
+// outputs to HBM (last step). LOGV is the tile's log2 vector width when known
+// at compile time (then LDS addresses are a base plus immediate offsets), or
+// -1 to read it from the tile.
+template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE, int LOGV>
+__host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, const PassLane& l,
+                                                  uint32_t tid, uint32_t T, uint64_t* lds, const uint64_t* twtab)
 {
     constexpr int R = 1 << RL;
     constexpr int QL = BS - RL;
-    const uint32_t logV = t.logV;
-    const uint32_t V = 1u << logV;
+    // A thread takes U items per round and issues all their reads before any
+    // arithmetic, so that U * R reads are in flight per thread.
+    constexpr int U = 2;
+    const uint32_t logV = LOGV >= 0 ? (uint32_t)LOGV : t.logV;
     const uint32_t items = (1u << (S - RL)) << logV;
-    for (uint32_t it = tid; it < items; it += T) {
-        const uint32_t v = it & (V - 1);
-        const uint32_t rest = it >> logV;
-        const uint32_t q = rest & ((1u << QL) - 1);
-        const uint32_t base = ((rest >> QL) << BS) + q;
-        uint64_t x[R];
+    const uint32_t v = l.v;
+    for (uint32_t it0 = tid; it0 < items; it0 += U * T) {
+        uint64_t x[U][R];
+        uint64_t tw[U][R];  // step twiddles w_{2^BS}^(f q), read with the data
+        uint32_t base[U], q[U];
+        bool live[U];
 #pragma unroll
-        for (int k = 0; k < R; k++) {
-            const uint32_t pos = base + ((uint32_t)k << QL);
-            if (FROM_GLOBAL) {
-                x[k] = k < KNZ ? pass_load_elem(a, t, pos, v) : 0;
-            } else {
-                ZK_BOUND((pos << logV) | v, (1u << S) << logV);
-                x[k] = lds[(pos << logV) | v];
+        for (int u = 0; u < U; u++) {
+            const uint32_t it = it0 + (uint32_t)u * T;
+            live[u] = it < items;
+            const uint32_t rest = it >> logV;
+            q[u] = rest & ((1u << QL) - 1);
+            base[u] = ((rest >> QL) << BS) + q[u];
+            if (!live[u]) continue;
+            const uint64_t gbase = l.in_base + (uint64_t)base[u] * a.in_stride;
+            const uint32_t lbase = (base[u] << logV) | v;
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+                const uint32_t pos = base[u] + ((uint32_t)k << QL);
+                if (FROM_GLOBAL) {
+                    if (k < KNZ && (!a.check_rows || pos < l.pos_lim)) {
+                        const uint64_t idx = gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride;
+                        ZK_BOUND(idx, a.in_len);
+                        x[u][k] = a.in[idx];
+                    } else {
+                        x[u][k] = 0;
+                    }
+                } else {
+                    const uint32_t li = lbase + (((uint32_t)k << QL) << logV);
+                    ZK_BOUND(li, (1u << S) << logV);
+                    x[u][k] = lds[li];
+                }
+            }
+            if (QL > 0) {
+#pragma unroll
+                for (int idx = 1; idx < R; idx++) {
+                    const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                    tw[u][idx] = a.w512[(f * q[u]) << (kStepTableLg - BS)];
+                }
             }
         }
-        dft_small<RL, INV>(x);
-        if (QL > 0 && q != 0) {
 #pragma unroll
-            for (int idx = 1; idx < R; idx++) {
-                const uint32_t f = bit_reverse((uint32_t)idx, RL);
-                x[idx] = gl_mul(x[idx], a.w512[(f * q) << (kStepTableLg - BS)]);
+        for (int u = 0; u < U; u++) {
+            if (!live[u]) continue;
+            dft_small<RL, INV>(x[u]);
+            if (QL > 0) {
+#pragma unroll
+                for (int idx = 1; idx < R; idx++) x[u][idx] = gl_mul(x[u][idx], tw[u][idx]);
             }
-        }
-#pragma unroll
-        for (int idx = 0; idx < R; idx++) {
-            const uint32_t f = bit_reverse((uint32_t)idx, RL);
-            const uint32_t pos = base + (f << QL);
             if (TO_GLOBAL) {
-                const uint64_t c = t.c0 + (v & ((1u << a.logC) - 1));
-                const uint64_t j2 = t.j20 + (v >> a.logC);
-                if (ROLE >= kRoleLast)
-                    pass_store_elem<ROLE>(a, digit_reverse<S>(pos), v, x[idx], twtab, t.nat0,
-                                          1ull << (a.L - a.s), c, 0);
-                else
-                    pass_store_elem<ROLE>(a, digit_reverse<S>(pos), v, x[idx], twtab, t.blk + j2,
-                                          t.N2, c, j2);
+                // QL == 0 here: base holds the leading digits, f the last one,
+                // which digit reversal moves to the top of i1.
+                const uint32_t i1b = digit_reverse<S>(base[u]);
+                const uint64_t obase = l.out_base + (uint64_t)i1b * a.out_stride;
+#pragma unroll
+                for (int idx = 0; idx < R; idx++) {
+                    const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                    const uint32_t fi = f << (S - RL);
+                    const uint32_t i1 = i1b + fi;
+                    uint64_t val = x[u][idx];
+                    if (ROLE == kRoleTable) {
+                        ZK_BOUND(i1, 1u << a.s);
+                        val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
+                    } else if (ROLE == kRoleTwiddle) {
+                        const uint64_t ex = (uint64_t)i1 * l.j2;
+                        if (ex) val = gl_mul(val, pass_root_pow(a, ex));
+                    } else {
+                        if (ROLE == kRoleLastScale) val = gl_mul(val, a.scale);
+                        val = gl_canon(val);
+                    }
+                    const uint64_t oidx = obase + (uint64_t)fi * a.out_stride;
+                    ZK_BOUND(oidx, a.out_len);
+                    a.out[oidx] = val;
+                }
             } else {
-                ZK_BOUND((pos << logV) | v, (1u << S) << logV);
-                lds[(pos << logV) | v] = x[idx];
+                const uint32_t lbase = (base[u] << logV) | v;
+#pragma unroll
+                for (int idx = 0; idx < R; idx++) {
+                    const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                    const uint32_t li = lbase + ((f << QL) << logV);
+                    ZK_BOUND(li, (1u << S) << logV);
+                    lds[li] = x[u][idx];
+                }
             }
         }
     }
@@ -347,25 +390,26 @@ __host__ __device__ __forceinline__ void pass_prologue(const PassArgs& a, const 
 
 // Step `k` of the S-point sub-DFT (k < pass_steps<S>()). The caller puts a
 // workgroup barrier between consecutive steps.
-template <int S, int KNZ, bool INV, int ROLE>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV>
 __host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, const PassTile& t,
-                                                   uint32_t tid, uint32_t T, uint64_t* lds)
+                                                   const PassLane& l, uint32_t tid, uint32_t T,
+                                                   uint64_t* lds)
 {
     using Rd = Radix<S>;
     constexpr int n = Rd::n;
     const uint64_t* tab = ROLE == kRoleTable ? lds + ((1u << S) << t.logV) : nullptr;
     if (k == 0) {
         if (n == 1)
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, true, ROLE>(a, t, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, true, ROLE, LOGV>(a, t, l, tid, T, lds, nullptr);
         else
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, false, ROLE>(a, t, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, false, ROLE, LOGV>(a, t, l, tid, T, lds, nullptr);
     } else if (k == 1) {
         if (n == 2)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE>(a, t, tid, T, lds, tab);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, tab);
         else if (n == 3)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false, ROLE>(a, t, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false, ROLE, LOGV>(a, t, l, tid, T, lds, nullptr);
     } else if (k == 2) {
-        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE>(a, t, tid, T, lds, tab);
+        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, tab);
     }
 }
 

@@ -75,6 +75,27 @@ inline Plan make_plan(uint32_t L, uint64_t w)
     return p;
 }
 
+// Non-zero inputs among the R = 2^r0 inputs of a step-0 radix DFT: an LDE's
+// first pass reads h = n / blowup rows, so inputs k >= R / blowup are zero.
+inline int pass_knz(const PassArgs& a)
+{
+    const int r0 = a.s <= 3 ? (int)a.s : 3;
+    const uint64_t n = 1ull << a.L;
+    const uint64_t R = 1ull << r0;
+    if (a.in_rows >= n || a.B != a.L) return (int)R;
+    // rows j1 N2 + j2 < in_rows <=> j1 < in_rows / N2 (a power of two here)
+    const uint64_t n2 = 1ull << (a.B - a.s);
+    const uint64_t j1_nz = (a.in_rows + n2 - 1) / n2;  // j1 < j1_nz can be non-zero
+    const uint64_t q_span = 1ull << (a.s - r0);
+    uint64_t knz = (j1_nz + q_span - 1) / q_span;
+    if (knz > R) knz = R;
+    if (knz < 1) knz = 1;
+    // round up to a power of two (template instances exist for 1, 2, 4, 8)
+    uint64_t p2 = 1;
+    while (p2 < knz) p2 <<= 1;
+    return (int)p2;
+}
+
 // Arguments of pass i. Passes 0..np-2 read `in` (pass 0) or `tmp` and write
 // `tmp` in place; the last pass reads `tmp` (or `in` when np == 1) and writes
 // `out` in natural order. B is the block log-size entering pass i.
@@ -106,7 +127,24 @@ inline PassArgs pass_args(const Plan& p, uint32_t i, uint32_t B, uint64_t w, con
     a.last = last ? 1 : 0;
     a.np = p.np;
     for (int k = 0; k < 8; k++) a.sb[k] = p.sb[k];
+    const uint64_t N2 = 1ull << logN2;
+    a.in_stride = (uint32_t)(N2 * w);
+    a.out_stride = (uint32_t)((last ? (n >> a.s) : N2) * w);
+    // Step 0 reads points j1 < KNZ 2^(s - r0) of each tile, i.e. rows below
+    // KNZ 2^(s - r0) N2 (first pass, a single block); they all hold data unless
+    // the input is shorter.
+    const uint32_t r0 = a.s <= 3 ? a.s : 3;
+    const uint64_t knz = (uint64_t)pass_knz(a);
+    a.check_rows = (knz << (a.s - r0)) * N2 > a.in_rows ? 1 : 0;
     return a;
+}
+
+// The pass strides of a plan fit the 32-bit fields of PassArgs.
+inline bool plan_fits(const Plan& p, uint64_t w)
+{
+    const uint64_t n = 1ull << p.L;
+    return w < (1ull << 32) && (n / (1ull << p.sb[p.np - 1])) * w < (1ull << 32) &&
+           (n >> p.sb[0]) * w < (1ull << 32);
 }
 
 // LDS of a pass: the N1 x V tile, unless the sub-DFT is a single step.
@@ -116,27 +154,6 @@ inline size_t pass_lds_bytes(const PassArgs& a)
     size_t words = (size_t)1 << (a.s + a.logC + a.logJ);
     if (pass_uses_twtab(a)) words += (size_t)1 << a.s;
     return words * 8;
-}
-
-// Non-zero inputs among the R = 2^r0 inputs of a step-0 radix DFT: an LDE's
-// first pass reads h = n / blowup rows, so inputs k >= R / blowup are zero.
-inline int pass_knz(const PassArgs& a)
-{
-    const int r0 = a.s <= 3 ? (int)a.s : 3;
-    const uint64_t n = 1ull << a.L;
-    const uint64_t R = 1ull << r0;
-    if (a.in_rows >= n || a.B != a.L) return (int)R;
-    // rows j1 N2 + j2 < in_rows <=> j1 < in_rows / N2 (a power of two here)
-    const uint64_t n2 = 1ull << (a.B - a.s);
-    const uint64_t j1_nz = (a.in_rows + n2 - 1) / n2;  // j1 < j1_nz can be non-zero
-    const uint64_t q_span = 1ull << (a.s - r0);
-    uint64_t knz = (j1_nz + q_span - 1) / q_span;
-    if (knz > R) knz = R;
-    if (knz < 1) knz = 1;
-    // round up to a power of two (template instances exist for 1, 2, 4, 8)
-    uint64_t p2 = 1;
-    while (p2 < knz) p2 <<= 1;
-    return (int)p2;
 }
 
 }  // namespace zk
