@@ -207,6 +207,92 @@ __host__ __device__ __forceinline__ void gl_mul2(uint64_t a, uint64_t b, uint64_
 #endif
 }
 
+// --- Linear-layer helpers whose device forms use the carry and borrow masks
+// of the 32-bit add/sub instructions directly (two wait states between the
+// VALU that writes a mask and the VALU that reads it).
+
+// a - b for b <= p and any a: one borrow at most (a - b + 2^64 >= eps).
+__host__ __device__ __forceinline__ uint64_t gl_sub_small(uint64_t a, uint64_t b)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint32_t d0, d1, e;
+    uint64_t k;
+    asm("v_sub_co_u32_e64 %0, %3, %4, %6\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %5, %7, %3\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
+        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %1, 0, %3"
+        : "=&v"(d0), "=&v"(d1), "=&v"(e), "=&s"(k)
+        : "v"((uint32_t)a), "v"((uint32_t)(a >> 32)), "v"((uint32_t)b), "v"((uint32_t)(b >> 32)));
+    return ((uint64_t)d1 << 32) | d0;
+#else
+    const uint64_t d = a - b;
+    return a < b ? d - EPS : d;
+#endif
+}
+
+// a - b for any a, b: the first borrow folds back as - eps, which borrows
+// again only when a - b + 2^64 < eps; the third subtraction cannot borrow.
+__host__ __device__ __forceinline__ uint64_t gl_sub2(uint64_t a, uint64_t b)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint32_t d0, d1, e;
+    uint64_t k;
+    asm("v_sub_co_u32_e64 %0, %3, %4, %6\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %5, %7, %3\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
+        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %1, 0, %3\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
+        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %1, 0, %3"
+        : "=&v"(d0), "=&v"(d1), "=&v"(e), "=&s"(k)
+        : "v"((uint32_t)a), "v"((uint32_t)(a >> 32)), "v"((uint32_t)b), "v"((uint32_t)(b >> 32)));
+    return ((uint64_t)d1 << 32) | d0;
+#else
+    return gl_sub(a, b);
+#endif
+}
+
+// s + m eps for any s and m < 2^32: the product-add wraps at most once, and
+// after a wrap the value is below m eps <= 2^64 - 2^33, so + eps cannot wrap.
+__host__ __device__ __forceinline__ uint64_t gl_add_meps(uint64_t s, uint32_t m)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint64_t S, k;
+    uint32_t c;
+    asm("v_mad_u64_u32 %0, %1, %3, -1, %4\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, 1, %1\n\t"
+        "v_mad_u64_u32 %0, %1, %2, -1, %0"
+        : "=&v"(S), "=&s"(k), "=&v"(c)
+        : "v"(m), "v"(s));
+    return S;
+#else
+    return gl_add(s, (uint64_t)m * EPS);
+#endif
+}
+
+// acc + x for a 64-bit running sum of 32-bit values (one v_mad_u64_u32).
+__host__ __device__ __forceinline__ uint64_t acc32(uint64_t acc, uint32_t x)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint64_t r, k;
+    asm("v_mad_u64_u32 %0, %1, %2, 1, %3" : "=&v"(r), "=s"(k) : "v"(x), "v"(acc));
+    return r;
+#else
+    return acc + x;
+#endif
+}
+
 // x * 2^-k for 1 <= k <= 32, any x < 2^64:
 // x = q 2^k + r, r 2^-k = -r 2^(96-k) = -(m * eps) with m = r 2^(32-k) < 2^32,
 // and -(m * eps) = p - m 2^32 + m = (2^32 - 1 - m) 2^32 + (m + 1).

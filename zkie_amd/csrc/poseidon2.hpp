@@ -86,47 +86,51 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
 }
 
 // One internal round: st0 <- (st0 + rc)^7, then st_i <- sum + V_i st_i.
-// The 15 scaled terms and the partial sum of st[1..15] do not depend on the
-// S-box, so they are formed first; the full sum is made canonical so that
-// every "sum + t" below needs a single wrap correction.
+// The round sum is formed from 32-bit halves (two 64-bit running sums, one
+// v_mad_u64_u32 per half) and made canonical, so that the lanes can use
+// single-correction forms:
+//   V = -2^-k (k = 3, 4, 5): x 2^-k = q - m eps with q = x >> k,
+//     m = (x mod 2^k) 2^(32-k), so sum - x 2^-k = (sum + m eps) - q;
+//   V = 2^-32: sum + x 2^-32 = (sum + x.hi) - x.lo eps, where sum + x.hi
+//     cannot wrap (sum <= p - 1) and x.lo eps < p;
+//   the other negative lanes subtract with gl_sub2.
 template <bool DIAG15_IS_INV_2_32>
 __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t rc, uint64_t diag15)
 {
-    Acc s = acc_of(st[1]);
+    uint64_t slo = (uint32_t)st[1], shi = st[1] >> 32;
 #pragma unroll
-    for (int i = 2; i < 16; i++) s = acc_add(s, st[i]);
-    const uint64_t t2 = gl_shl<1>(st[2]);                    //  2
-    const uint64_t t3 = gl_halve(st[3]);                     //  1/2
-    const uint64_t t4 = gl_add_shl<1>(st[4], st[4]);         //  3
-    const uint64_t t5 = gl_shl<2>(st[5]);                    //  4
-    const uint64_t t6 = gl_halve(st[6]);                     // -1/2
-    const uint64_t t7 = gl_add_shl<1>(st[7], st[7]);         // -3
-    const uint64_t t8 = gl_shl<2>(st[8]);                    // -4
-    const uint64_t t9 = gl_mul_inv_pow2<3>(st[9]);           //  1/2^3
-    const uint64_t t10 = gl_mul_inv_pow2<4>(st[10]);         //  1/2^4
-    const uint64_t t11 = gl_mul_inv_pow2<5>(st[11]);         //  1/2^5
-    const uint64_t t12 = gl_mul_inv_pow2<3>(st[12]);         // -1/2^3
-    const uint64_t t13 = gl_mul_inv_pow2<4>(st[13]);         // -1/2^4
-    const uint64_t t14 = gl_mul_inv_pow2<5>(st[14]);         // -1/2^5
-    const uint64_t t15 = DIAG15_IS_INV_2_32 ? gl_mul_inv_pow2<32>(st[15]) : gl_mul(st[15], diag15);
+    for (int i = 2; i < 16; i++) {
+        slo = acc32(slo, (uint32_t)st[i]);
+        shi = acc32(shi, (uint32_t)(st[i] >> 32));
+    }
     const uint64_t x0 = sbox7(gl_add_small(st[0], rc));
-    const uint64_t sum = gl_canon_fast(acc_reduce(acc_add(s, x0)));
-    st[0] = gl_sub(sum, gl_shl<1>(x0));                      // -2
-    st[1] = gl_add_small(st[1], sum);                        //  1
-    st[2] = gl_add_small(t2, sum);
-    st[3] = gl_add_small(t3, sum);
-    st[4] = gl_add_small(t4, sum);
-    st[5] = gl_add_small(t5, sum);
-    st[6] = gl_sub(sum, t6);
-    st[7] = gl_sub(sum, t7);
-    st[8] = gl_sub(sum, t8);
-    st[9] = gl_add_small(t9, sum);
-    st[10] = gl_add_small(t10, sum);
-    st[11] = gl_add_small(t11, sum);
-    st[12] = gl_sub(sum, t12);
-    st[13] = gl_sub(sum, t13);
-    st[14] = gl_sub(sum, t14);
-    st[15] = gl_add_small(t15, sum);                         //  diag15
+    slo = acc32(slo, (uint32_t)x0);
+    shi = acc32(shi, (uint32_t)(x0 >> 32));
+    // sum = slo + shi 2^32 = slo + (shi.lo << 32) + shi.hi 2^64, and 2^64 = eps
+    const uint64_t t = slo + (shi << 32);
+    const uint32_t k = (uint32_t)(shi >> 32) + (t < slo ? 1u : 0u);
+    const uint64_t sum = gl_canon_fast(gl_add_meps(t, k));
+
+    const uint64_t x15 = st[15];
+    st[0] = gl_sub2(sum, gl_shl<1>(x0));                                   // -2
+    st[1] = gl_add_small(st[1], sum);                                      //  1
+    st[2] = gl_add_shl<1>(sum, st[2]);                                     //  2
+    st[3] = gl_add_small(gl_halve(st[3]), sum);                            //  1/2
+    st[4] = gl_add_small(gl_add_shl<1>(st[4], st[4]), sum);                //  3
+    st[5] = gl_add_shl<2>(sum, st[5]);                                     //  4
+    st[6] = gl_sub2(sum, gl_halve(st[6]));                                 // -1/2
+    st[7] = gl_sub2(sum, gl_add_shl<1>(st[7], st[7]));                     // -3
+    st[8] = gl_sub2(sum, gl_shl<2>(st[8]));                                // -4
+    st[9] = gl_add_small(gl_mul_inv_pow2<3>(st[9]), sum);                  //  1/2^3
+    st[10] = gl_add_small(gl_mul_inv_pow2<4>(st[10]), sum);                //  1/2^4
+    st[11] = gl_add_small(gl_mul_inv_pow2<5>(st[11]), sum);                //  1/2^5
+    st[12] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[12] << 29), st[12] >> 3);  // -1/2^3
+    st[13] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[13] << 28), st[13] >> 4);  // -1/2^4
+    st[14] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[14] << 27), st[14] >> 5);  // -1/2^5
+    if (DIAG15_IS_INV_2_32)
+        st[15] = gl_sub_small(acc32(sum, (uint32_t)(x15 >> 32)), (uint64_t)(uint32_t)x15 * EPS);
+    else
+        st[15] = gl_add_small(gl_mul(x15, diag15), sum);
 }
 
 template <bool DIAG15_IS_INV_2_32>
