@@ -293,6 +293,41 @@ __host__ __device__ __forceinline__ uint64_t acc32(uint64_t acc, uint32_t x)
 #endif
 }
 
+// acc + x * M for a 64-bit running sum of 32-bit values, M a small constant.
+template <int M>
+__host__ __device__ __forceinline__ uint64_t acc32m(uint64_t acc, uint32_t x)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    static_assert(M >= 1 && M <= 64, "inline constant");
+    uint64_t r, k;
+    asm("v_mad_u64_u32 %0, %1, %2, %4, %3" : "=&v"(r), "=s"(k) : "v"(x), "v"(acc), "i"(M));
+    return r;
+#else
+    return acc + (uint64_t)x * M;
+#endif
+}
+
+// A + B 2^32 mod p for A, B < 2^63 (sums of 32-bit halves): with
+// t = A + (B.lo << 32) and its carry c, the value is t + (B.hi + c) 2^64
+// and 2^64 = eps.
+__host__ __device__ __forceinline__ uint64_t gl_from_halves(uint64_t A, uint64_t B)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint32_t th, k;
+    uint64_t m;
+    asm("v_add_co_u32_e64 %0, %2, %3, %4\n\t"
+        "s_nop 1\n\t"
+        "v_addc_co_u32_e64 %1, %2, %5, 0, %2"
+        : "=&v"(th), "=&v"(k), "=&s"(m)
+        : "v"((uint32_t)(A >> 32)), "v"((uint32_t)B), "v"((uint32_t)(B >> 32)));
+    return gl_add_meps(((uint64_t)th << 32) | (uint32_t)A, k);
+#else
+    const uint64_t t = A + (B << 32);
+    const uint32_t k = (uint32_t)(B >> 32) + (t < A ? 1u : 0u);
+    return gl_add(t, (uint64_t)k * EPS);
+#endif
+}
+
 // x * 2^-k for 1 <= k <= 32, any x < 2^64:
 // x = q 2^k + r, r 2^-k = -r 2^(96-k) = -(m * eps) with m = r 2^(32-k) < 2^32,
 // and -(m * eps) = p - m 2^32 + m = (2^32 - 1 - m) 2^32 + (m + 1).

@@ -162,7 +162,7 @@ __device__ __forceinline__ void hash_row(const uint64_t* __restrict__ row, uint6
 
 // Leaf digests of rows [row0, row_end).
 template <int W, bool D15>
-__global__ __launch_bounds__(256) void leaf_kernel(const uint64_t* __restrict__ mat,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void leaf_kernel(const uint64_t* __restrict__ mat,
                                                    uint64_t* __restrict__ digests, uint64_t row0,
                                                    uint64_t row_end, uint64_t w)
 {
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void leaf_kernel(const uint64_t* __restrict__ 
 // Parents [from, to) of `step` children each; slots [to, pad_to) get the
 // zero digest (merkle_tree.rs:393-396 default digest padding).
 template <bool D15>
-__global__ __launch_bounds__(256) void compress_kernel(const uint64_t* __restrict__ prev,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void compress_kernel(const uint64_t* __restrict__ prev,
                                                        uint64_t* __restrict__ next, uint64_t from,
                                                        uint64_t to, uint64_t pad_to, uint32_t step)
 {

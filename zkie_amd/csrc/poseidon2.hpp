@@ -67,21 +67,56 @@ __host__ __device__ __forceinline__ void mat4_lazy(const uint64_t* x, Acc* y)
     y[2] = acc_add(t01233, t23);                  // x0 + x1 + 2x2 + 3x3
 }
 
-// st <- mds_light16(st) (+ rc if given), each output reduced once.
+// mat4 on one 32-bit half of four lanes, into 64-bit sums (coefficients
+// 1, 2, 3, so no sum can carry).
+__host__ __device__ __forceinline__ void mat4_half(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                                   uint64_t* y)
+{
+    const uint64_t t01 = acc32m<1>(x0, x1);
+    const uint64_t t23 = acc32m<1>(x2, x3);
+    const uint64_t t0123 = t01 + t23;
+    const uint64_t t01123 = acc32m<1>(t0123, x1);
+    const uint64_t t01233 = acc32m<1>(t0123, x3);
+    y[3] = acc32m<2>(t01233, x0);  // 3x0 + x1 + x2 + 2x3
+    y[1] = acc32m<2>(t01123, x2);  // x0 + 2x1 + 3x2 + x3
+    y[0] = t01123 + t01;           // 2x0 + 3x1 + x2 + x3
+    y[2] = t01233 + t23;           // x0 + x1 + 2x2 + 3x3
+}
+
+// mat4 of each lane group on one half, and the column sums
+// sums[k] = sum_g y_{4g + k}; output i is then y_i + sums[i mod 4].
+template <bool HI>
+__host__ __device__ __forceinline__ void mds_half(const uint64_t* st, uint64_t* y, uint64_t* sums)
+{
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) {
+        if (HI)
+            mat4_half((uint32_t)(st[j] >> 32), (uint32_t)(st[j + 1] >> 32), (uint32_t)(st[j + 2] >> 32),
+                      (uint32_t)(st[j + 3] >> 32), y + j);
+        else
+            mat4_half((uint32_t)st[j], (uint32_t)st[j + 1], (uint32_t)st[j + 2], (uint32_t)st[j + 3], y + j);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) sums[k] = (y[k] + y[4 + k]) + (y[8 + k] + y[12 + k]);
+}
+
+// st <- mds_light16(st) (+ rc if given). Both 32-bit halves of the state go
+// through the layer as exact 64-bit sums (at most 35 (2^32 - 1) + 2^32 each),
+// and each output is reduced once from its two sums as it is formed.
 template <bool ADD_RC>
 __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_t* rc)
 {
-    Acc y[16];
-#pragma unroll
-    for (int j = 0; j < 16; j += 4) mat4_lazy(st + j, y + j);
-    Acc sums[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) sums[k] = acc_add(acc_add(y[k], y[4 + k]), acc_add(y[8 + k], y[12 + k]));
+    uint64_t ylo[16], yhi[16], slo[4], shi[4];
+    mds_half<false>(st, ylo, slo);
+    mds_half<true>(st, yhi, shi);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        Acc t = acc_add(y[i], sums[i & 3]);
-        if (ADD_RC) t = acc_add(t, rc[i]);
-        st[i] = acc_reduce(t);
+        uint64_t A = ylo[i] + slo[i & 3], B = yhi[i] + shi[i & 3];
+        if (ADD_RC) {
+            A = acc32m<1>(A, (uint32_t)rc[i]);
+            B = acc32m<1>(B, (uint32_t)(rc[i] >> 32));
+        }
+        st[i] = gl_from_halves(A, B);
     }
 }
 
