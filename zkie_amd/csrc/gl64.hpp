@@ -341,6 +341,20 @@ __host__ __device__ __forceinline__ uint64_t gl_mul_inv_pow2(uint64_t x)
     return gl_add_small(q, y) ;
 }
 
+// x * 2^24: x << 24 plus the shifted-out bits hi < 2^24 at weight 2^64 = eps.
+__host__ __device__ __forceinline__ uint64_t gl_mul_2e24(uint64_t x)
+{
+    return gl_add_meps(x << 24, (uint32_t)(x >> 40));
+}
+
+// x * 2^48: hi = x >> 16 (48 bits) at weight 2^64; hi eps = hi.lo eps + hi.hi 2^32 eps
+// and 2^32 eps = 2^64 - 2^32 = -1, so x 2^48 = (x << 48) + hi.lo eps - hi.hi.
+__host__ __device__ __forceinline__ uint64_t gl_mul_2e48(uint64_t x)
+{
+    const uint64_t hi = x >> 16;
+    return gl_sub_small(gl_add_meps(x << 48, (uint32_t)hi), hi >> 32);
+}
+
 // Canonical representative: x >= p exactly when x + eps wraps.
 __host__ __device__ __forceinline__ uint64_t gl_canon_fast(uint64_t x)
 {

@@ -163,63 +163,75 @@ __host__ __device__ __forceinline__ uint32_t digit_reverse(uint32_t pos)
     return f;
 }
 
-// Roots of unity used inside the 8- and 4-point DFTs.
-template <bool INV>
-struct SmallRoots {
-    static constexpr uint64_t w4 = INV ? 0xFFFEFFFF00000001ull : 0x0001000000000000ull;
-    static constexpr uint64_t w8 = INV ? 0x000000FFFFFFFF00ull : 0xFFFFFFFEFF000001ull;
-    static constexpr uint64_t w8_3 = INV ? 0x0000000001000000ull : 0xFFFFFEFF00000101ull;
-};
+// Roots of unity inside the 8- and 4-point DFTs are signed powers of two:
+// forward w4 = 2^48, w8 = -2^24, w8^3 = -2^72 = 2^-24; inverse w4 = -2^48,
+// w8 = 2^72 = -2^-24, w8^3 = 2^24 (2^96 = -1). A butterfly output
+// (u - v) w with w = -2^k is formed as (v - u) 2^k, so every twiddle inside
+// a small DFT is a shift form (gl_mul_2e24, gl_mul_2e48, gl_mul_inv_pow2<24>).
+template <bool INV, int P8>
+__host__ __device__ __forceinline__ uint64_t dif_lower8(uint64_t u, uint64_t v)
+{
+    // lower output of a radix-2 butterfly of the 8-point DFT, twiddle w8^P8
+    if (P8 == 0) return gl_sub2(u, v);
+    if (!INV) {
+        if (P8 == 1) return gl_mul_2e24(gl_sub2(v, u));         // -2^24
+        if (P8 == 2) return gl_mul_2e48(gl_sub2(u, v));         //  2^48
+        return gl_mul_inv_pow2<24>(gl_sub2(u, v));              //  2^-24
+    } else {
+        if (P8 == 1) return gl_mul_inv_pow2<24>(gl_sub2(v, u)); // -2^-24
+        if (P8 == 2) return gl_mul_2e48(gl_sub2(v, u));         // -2^48
+        return gl_mul_2e24(gl_sub2(u, v));                      //  2^24
+    }
+}
 
 // In-register R-point DFT (radix-2 DIF); x[idx] ends up holding frequency
 // bit_reverse(idx, log2 R).
 template <int RLOG, bool INV>
 __host__ __device__ __forceinline__ void dft_small(uint64_t* x)
 {
-    using W = SmallRoots<INV>;
     if (RLOG == 3) {
-        const uint64_t tw[4] = {1, W::w8, W::w4, W::w8_3};
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const uint64_t u = x[p], v = x[p + 4];
-            x[p] = gl_add(u, v);
-            const uint64_t d = gl_sub(u, v);
-            x[p + 4] = p == 0 ? d : gl_mul(d, tw[p]);
+        {
+            const uint64_t u0 = x[0], v0 = x[4], u1 = x[1], v1 = x[5];
+            const uint64_t u2 = x[2], v2 = x[6], u3 = x[3], v3 = x[7];
+            x[0] = gl_add(u0, v0);
+            x[1] = gl_add(u1, v1);
+            x[2] = gl_add(u2, v2);
+            x[3] = gl_add(u3, v3);
+            x[4] = dif_lower8<INV, 0>(u0, v0);
+            x[5] = dif_lower8<INV, 1>(u1, v1);
+            x[6] = dif_lower8<INV, 2>(u2, v2);
+            x[7] = dif_lower8<INV, 3>(u3, v3);
         }
 #pragma unroll
         for (int h = 0; h < 8; h += 4) {
-#pragma unroll
-            for (int p = 0; p < 2; p++) {
-                const uint64_t u = x[h + p], v = x[h + p + 2];
-                x[h + p] = gl_add(u, v);
-                const uint64_t d = gl_sub(u, v);
-                x[h + p + 2] = p == 0 ? d : gl_mul(d, W::w4);
-            }
+            const uint64_t u0 = x[h], v0 = x[h + 2], u1 = x[h + 1], v1 = x[h + 3];
+            x[h] = gl_add(u0, v0);
+            x[h + 1] = gl_add(u1, v1);
+            x[h + 2] = dif_lower8<INV, 0>(u0, v0);
+            x[h + 3] = dif_lower8<INV, 2>(u1, v1);  // w4 = w8^2
         }
 #pragma unroll
         for (int q = 0; q < 8; q += 2) {
             const uint64_t u = x[q], v = x[q + 1];
             x[q] = gl_add(u, v);
-            x[q + 1] = gl_sub(u, v);
+            x[q + 1] = gl_sub2(u, v);
         }
     } else if (RLOG == 2) {
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            const uint64_t u = x[p], v = x[p + 2];
-            x[p] = gl_add(u, v);
-            const uint64_t d = gl_sub(u, v);
-            x[p + 2] = p == 0 ? d : gl_mul(d, W::w4);
-        }
+        const uint64_t u0 = x[0], v0 = x[2], u1 = x[1], v1 = x[3];
+        x[0] = gl_add(u0, v0);
+        x[1] = gl_add(u1, v1);
+        x[2] = dif_lower8<INV, 0>(u0, v0);
+        x[3] = dif_lower8<INV, 2>(u1, v1);
 #pragma unroll
         for (int q = 0; q < 4; q += 2) {
             const uint64_t u = x[q], v = x[q + 1];
             x[q] = gl_add(u, v);
-            x[q + 1] = gl_sub(u, v);
+            x[q + 1] = gl_sub2(u, v);
         }
     } else if (RLOG == 1) {
         const uint64_t u = x[0], v = x[1];
         x[0] = gl_add(u, v);
-        x[1] = gl_sub(u, v);
+        x[1] = gl_sub2(u, v);
     }
 }
 
