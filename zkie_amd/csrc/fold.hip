@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "gl64.hpp"
+#include "row_stage.hpp"
 #include "runtime.hpp"
 
 namespace zk {
@@ -21,30 +22,41 @@ __global__ __launch_bounds__(256) void fold_kernel(const uint64_t* __restrict__ 
                                                    const uint64_t* __restrict__ eq,
                                                    uint64_t* __restrict__ out)
 {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= h) return;
     constexpr int Wd = 1 << K;
+    constexpr int RW = EXT ? 2 * Wd : Wd;  // u64 per row
+    const uint64_t* row;
+    uint64_t t;
+    if constexpr (RW == 8 || RW == 16) {
+        // rows of 64 or 128 bytes: staged through LDS so HBM serves each once
+        __shared__ uint64_t tile[256 * (RW + 1)];
+        const uint64_t first = (uint64_t)blockIdx.x * 256;
+        const uint32_t nrows = h - first < 256 ? (uint32_t)(h - first) : 256u;
+        stage_rows<RW>(mat, first, nrows, tile);
+        if (threadIdx.x >= nrows) return;
+        t = first + threadIdx.x;
+        row = tile + threadIdx.x * (RW + 1);
+    } else {
+        t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (t >= h) return;
+        row = mat + t * RW;
+    }
     Acc s0 = acc_of(0), s1 = acc_of(0);
     if (!EXT) {
-        const ulonglong2* row = reinterpret_cast<const ulonglong2*>(mat + t * Wd);
-#pragma unroll
-        for (int j2 = 0; j2 < Wd / 2; j2++) {
-            const ulonglong2 x = row[j2];
-            s0 = acc_add(s0, gl_mul(eq[4 * j2 + 0], x.x));
-            s1 = acc_add(s1, gl_mul(eq[4 * j2 + 1], x.x));
-            s0 = acc_add(s0, gl_mul(eq[4 * j2 + 2], x.y));
-            s1 = acc_add(s1, gl_mul(eq[4 * j2 + 3], x.y));
-        }
-    } else {
-        const ulonglong2* row = reinterpret_cast<const ulonglong2*>(mat + t * 2 * Wd);
 #pragma unroll
         for (int j = 0; j < Wd; j++) {
-            const ulonglong2 y = row[j];
+            const uint64_t x = row[j];
+            s0 = acc_add(s0, gl_mul(eq[2 * j + 0], x));
+            s1 = acc_add(s1, gl_mul(eq[2 * j + 1], x));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < Wd; j++) {
+            const uint64_t y0 = row[2 * j], y1 = row[2 * j + 1];
             const uint64_t e0 = eq[2 * j], e1 = eq[2 * j + 1];
-            s0 = acc_add(s0, gl_mul(e0, y.x));
-            s0 = acc_add(s0, gl_mul7(gl_mul(e1, y.y)));
-            s1 = acc_add(s1, gl_mul(e0, y.y));
-            s1 = acc_add(s1, gl_mul(e1, y.x));
+            s0 = acc_add(s0, gl_mul(e0, y0));
+            s0 = acc_add(s0, gl_mul7(gl_mul(e1, y1)));
+            s1 = acc_add(s1, gl_mul(e0, y1));
+            s1 = acc_add(s1, gl_mul(e1, y0));
         }
     }
     reinterpret_cast<ulonglong2*>(out)[t] = make_ulonglong2(gl_canon(acc_reduce(s0)), gl_canon(acc_reduce(s1)));

@@ -307,6 +307,18 @@ __host__ __device__ __forceinline__ uint64_t acc32m(uint64_t acc, uint32_t x)
 #endif
 }
 
+// acc + x for a wave-uniform x (an SGPR operand, e.g. a round constant).
+__host__ __device__ __forceinline__ uint64_t acc32s(uint64_t acc, uint32_t x)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint64_t r, k;
+    asm("v_mad_u64_u32 %0, %1, %2, 1, %3" : "=&v"(r), "=s"(k) : "s"(x), "v"(acc));
+    return r;
+#else
+    return acc + x;
+#endif
+}
+
 // A + B 2^32 mod p for A, B < 2^63 (sums of 32-bit halves): with
 // t = A + (B.lo << 32) and its carry c, the value is t + (B.hi + c) 2^64
 // and 2^64 = eps.

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "poseidon2.hpp"
+#include "row_stage.hpp"
 #include "runtime.hpp"
 
 namespace zk {
@@ -160,17 +161,36 @@ __device__ __forceinline__ void hash_row(const uint64_t* __restrict__ row, uint6
     }
 }
 
-// Leaf digests of rows [row0, row_end).
+// Leaf digests of rows [row0, row_end). Rows of 8 or 16 elements are staged
+// through LDS (row_stage.hpp) so HBM serves each row once.
 template <int W, bool D15>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void leaf_kernel(const uint64_t* __restrict__ mat,
-                                                   uint64_t* __restrict__ digests, uint64_t row0,
-                                                   uint64_t row_end, uint64_t w)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void leaf_kernel(
+    const uint64_t* __restrict__ mat, uint64_t* __restrict__ digests, uint64_t row0, uint64_t row_end,
+    uint64_t w)
 {
-    const uint64_t row = row0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= row_end) return;
     uint64_t st[16];
-    hash_row<W, D15>(mat + row * (W > 0 ? (uint64_t)W : w), w, st);
-    store_digest(digests + row * 8, st);
+    if constexpr (W == 8 || W == 16) {
+        __shared__ uint64_t tile[256 * (W + 1)];
+        const uint64_t first = row0 + (uint64_t)blockIdx.x * 256;
+        const uint32_t nrows = row_end - first < 256 ? (uint32_t)(row_end - first) : 256u;
+        stage_rows<W>(mat, first, nrows, tile);
+        if (threadIdx.x >= nrows) return;
+        const uint64_t* row = tile + threadIdx.x * (W + 1);
+#pragma unroll
+        for (int i = 8; i < 16; i++) st[i] = 0;
+#pragma unroll 1
+        for (int b = 0; b < W / 8; b++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) st[i] = row[8 * b + i];
+            p2_permute<D15>(st, c_p2);
+        }
+        store_digest(digests + (first + threadIdx.x) * 8, st);
+    } else {
+        const uint64_t row = row0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (row >= row_end) return;
+        hash_row<W, D15>(mat + row * (W > 0 ? (uint64_t)W : w), w, st);
+        store_digest(digests + row * 8, st);
+    }
 }
 
 // Parents [from, to) of `step` children each; slots [to, pad_to) get the

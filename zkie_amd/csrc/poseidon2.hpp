@@ -113,8 +113,8 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
     for (int i = 0; i < 16; i++) {
         uint64_t A = ylo[i] + slo[i & 3], B = yhi[i] + shi[i & 3];
         if (ADD_RC) {
-            A = acc32m<1>(A, (uint32_t)rc[i]);
-            B = acc32m<1>(B, (uint32_t)(rc[i] >> 32));
+            A = acc32s(A, (uint32_t)rc[i]);
+            B = acc32s(B, (uint32_t)(rc[i] >> 32));
         }
         st[i] = gl_from_halves(A, B);
     }
