@@ -144,6 +144,35 @@ int zkie_merkle_open_pruned(const uint64_t *d_mat, uint64_t h, uint64_t w,
 int zkie_fold_rows(const uint64_t *d_mat, uint64_t h, uint32_t log_width, int is_ext,
                    const uint64_t *r, uint64_t *d_out, void *stream);
 
+/* Queried-row fold of a STIR round (p3-whir src/pcs/prover/mod.rs:265-290,
+ * Poly::eval_base / eval_ext of each opened row): the same fold as
+ * zkie_fold_rows applied to rows indices[0..n) (host, each < h) of the
+ * device matrix only; out (host) receives n EF elements (2n u64). */
+int zkie_fold_rows_at(const uint64_t *d_mat, uint64_t h, uint32_t log_width, int is_ext,
+                      const uint64_t *indices, uint64_t n, const uint64_t *r, uint64_t *out,
+                      void *stream);
+
+/* Multilinear evaluation of a device table of 2^num_vars entries (base, or
+ * EF flattened [c0, c1] when is_ext) at an EF point: sum_j eq(r, j) * v[j]
+ * with coordinate 0 the least-significant index bit (common/mle.rs:8-22).
+ * This is the out-of-domain answer `sumcheck_prover.eval(&point)` of a WHIR
+ * round (p3-whir src/pcs/prover/mod.rs:226-236); a p3 point, most
+ * significant variable first, is passed reversed, as the row fold does
+ * (prover/mod.rs:258-261). r (host): num_vars EF coordinates; out (host): one
+ * EF element (2 u64). The table never leaves HBM. */
+int zkie_mle_eval(const uint64_t *d_vals, uint32_t num_vars, int is_ext, const uint64_t *r,
+                  uint64_t *out, void *stream);
+
+/* Encoding of commit_extension (p3-whir src/pcs/committer/writer.rs:21-86):
+ * the 2^num_vars-entry table (base or EF) as a 2^(num_vars - log_width) x
+ * 2^log_width matrix, rows as stored (prefix = 0, VariableOrder::Suffix) or
+ * transposed (prefix = 1, VariableOrder::Prefix, writer.rs:43-71), zero-padded
+ * to 2^log_inv_rate times its height and transformed per base column
+ * (dft_algebra_batch). d_out receives 2^(num_vars + log_inv_rate) entries
+ * (times 2 u64 for EF), row-major. For prefix = 1 the buffers must not overlap. */
+int zkie_whir_encode(const uint64_t *d_poly, uint32_t num_vars, int is_ext, uint32_t log_width,
+                     uint32_t log_inv_rate, int prefix, uint64_t *d_out, void *stream);
+
 /* ------------------------------------------------------------------------
  * Synthetic inputs (host): XorShift64 of common/field.rs:17-36 seeded with
  * `seed`, embedded like common/fixed_point.rs:11-38. ZKIE_GEN_UNIFORM:

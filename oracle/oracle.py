@@ -71,6 +71,7 @@ def lib():
             "or_merkle_verify": (i32, [_u64p, u64, u64, _u64p, u64, _u64p]),
             "or_fold_rows": (None, [_u64p, u64, u32, i32, _u64p, _u64p]),
             "or_mle_eval_base": (u64, [_u64p, u32, _u64p]),
+            "or_mle_eval": (None, [_u64p, u32, ctypes.c_int, _u64p, _u64p]),
             "or_xorshift_next": (u64, [_u64p]),
             "or_xorshift_init": (None, [_u64p, u64]),
             "or_gen_uniform": (None, [u64, u64, _u64p]),
@@ -337,6 +338,30 @@ def fold_rows(mat: np.ndarray, k: int, r, is_ext: bool) -> np.ndarray:
 def mle_eval_base(values, point) -> int:
     v, pt = u64(values), u64(point)
     return lib().or_mle_eval_base(_p(v), pt.size, _p(pt))
+
+
+def mle_eval(values, point, is_ext: bool) -> np.ndarray:
+    """mle::eval (mle.rs:8-22) of 2^t base or flattened-EF values at t EF coordinates."""
+    v, pt = u64(values).reshape(-1), u64(point).reshape(-1)
+    t = pt.size // 2
+    assert v.size == (2 if is_ext else 1) << t
+    out = np.zeros(2, np.uint64)
+    lib().or_mle_eval(_p(v), t, 1 if is_ext else 0, _p(pt), _p(out))
+    return out
+
+
+def whir_encode(poly, num_vars: int, is_ext: bool, log_width: int, log_inv_rate: int,
+                prefix: bool) -> np.ndarray:
+    """commit_extension's encoding (p3-whir committer/writer.rs:21-86): the
+    table as 2^(n-k) rows x 2^k entries, rows as stored (Suffix) or
+    transposed so that entry (i, j) is poly[j 2^(n-k) + i] (Prefix,
+    writer.rs:43-71), zero-padded by 2^log_inv_rate and transformed per base
+    column (dft_algebra_batch is the base DFT of each component)."""
+    E = 2 if is_ext else 1
+    v = u64(poly).reshape(1 << num_vars, E)
+    rows, cols = 1 << (num_vars - log_width), 1 << log_width
+    m = v.reshape(cols, rows, E).transpose(1, 0, 2) if prefix else v.reshape(rows, cols, E)
+    return lde_batch(np.ascontiguousarray(m).reshape(rows, cols * E), log_inv_rate)
 
 
 # ---- inputs ------------------------------------------------------------------

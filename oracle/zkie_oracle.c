@@ -587,6 +587,31 @@ uint64_t or_mle_eval_base(const uint64_t *values, uint32_t t, const uint64_t *po
     return r;
 }
 
+void or_mle_eval(const uint64_t *values, uint32_t t, int is_ext, const uint64_t *point, uint64_t out[2])
+{
+    /* mle.rs:12-20: each round halves the table, buf[i] = a + r_v (b - a)
+     * for the pair (2i, 2i + 1), in EF. */
+    uint64_t n = 1ULL << t;
+    uint64_t *buf = (uint64_t *)malloc(2 * n * sizeof(uint64_t));
+    for (uint64_t i = 0; i < n; i++) {
+        buf[2 * i] = (is_ext ? values[2 * i] : values[i]) % OR_P;
+        buf[2 * i + 1] = is_ext ? values[2 * i + 1] % OR_P : 0;
+    }
+    for (uint32_t v = 0; v < t; v++) {
+        uint64_t half = n / 2;
+        for (uint64_t i = 0; i < half; i++) {
+            uint64_t d[2], m[2];
+            ef_sub(buf + 4 * i + 2, buf + 4 * i, d);
+            or_ef_mul(point + 2 * v, d, m);
+            ef_add(buf + 4 * i, m, buf + 2 * i);
+        }
+        n = half;
+    }
+    out[0] = buf[0];
+    out[1] = buf[1];
+    free(buf);
+}
+
 void or_fold_rows(const uint64_t *mat, uint64_t h, uint32_t k, int is_ext, const uint64_t *r,
                   uint64_t *out)
 {

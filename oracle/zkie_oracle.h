@@ -110,6 +110,10 @@ void or_fold_rows(const uint64_t *mat, uint64_t h, uint32_t k, int is_ext, const
                   uint64_t *out);
 /* mle::eval over base values and base point (mle.rs:8-22). */
 uint64_t or_mle_eval_base(const uint64_t *values, uint32_t t, const uint64_t *point);
+/* mle::eval (mle.rs:8-22) over base (is_ext = 0) or EF values at an EF point
+ * (t coordinates, 2t u64), variable 0 first (the least-significant bit):
+ * the out-of-domain answer of a WHIR round. out: one EF element. */
+void or_mle_eval(const uint64_t *values, uint32_t t, int is_ext, const uint64_t *point, uint64_t out[2]);
 
 /* ---- inputs (field.rs:17-36, fixed_point.rs:11-38) ---- */
 uint64_t or_xorshift_next(uint64_t *state);

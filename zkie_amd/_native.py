@@ -44,6 +44,9 @@ SIGNATURES = {
     "zkie_merkle_open_batch": [_vp, _u64, _u64, _vp, _u64p, _u64, _u64p, _u64p, _vp],
     "zkie_merkle_open_pruned": [_vp, _u64, _u64, _vp, _u64p, _u64, _u64p, _u64p, _u64, _u64p, _vp],
     "zkie_fold_rows": [_vp, _u64, _u32, _int, _u64p, _vp, _vp],
+    "zkie_fold_rows_at": [_vp, _u64, _u32, _int, _u64p, _u64, _u64p, _u64p, _vp],
+    "zkie_mle_eval": [_vp, _u32, _int, _u64p, _u64p, _vp],
+    "zkie_whir_encode": [_vp, _u32, _int, _u32, _u32, _int, _vp, _vp],
     "zkie_gen_inputs": [_u64, _u64, _int, _u64p],
     "zkie_profile_enable": [_int],
     "zkie_profile_reset": [],

@@ -148,7 +148,94 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
     return ZKIE_OK;
 }
 
+// Rows ids[0..n) (each `width` u64) gathered into dst.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint64_t* __restrict__ src, uint64_t width,
+                                                          const uint64_t* __restrict__ ids, uint64_t n,
+                                                          uint64_t* __restrict__ dst)
+{
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * width) return;
+    const uint64_t k = t / width, e = t % width;
+    dst[t] = src[ids[k] * width + e];
+}
+
+// Multilinear evaluation of a table of 2^t entries at r (t EF coordinates,
+// variable 0 the least-significant index bit): folds of at most six
+// variables at a time, each reading the previous EF table once.
+int mle_eval_device(const uint64_t* d_vals, uint32_t t, int is_ext, const uint64_t* r, uint64_t* out,
+                    hipStream_t s)
+{
+    if (t > 40 || !d_vals || !r || !out) return ZKIE_ERR_INVALID;
+    if (t == 0) {
+        out[1] = 0;
+        ZK_TRY(hipMemcpyAsync(out, d_vals, is_ext ? 16 : 8, hipMemcpyDeviceToHost, s));
+        ZK_TRY(hipStreamSynchronize(s));
+        out[0] = gl_canon(out[0]);
+        out[1] = gl_canon(out[1]);
+        return ZKIE_OK;
+    }
+    const uint32_t k0 = t < 6 ? t : 6;
+    const uint64_t first = 1ull << (t - k0);  // EF entries after the first fold
+    uint64_t* buf = (uint64_t*)workspace(WS_FOLD, 2 * first * 16);
+    if (!buf) return ZKIE_ERR_ALLOC;
+    uint64_t* ping = buf;
+    uint64_t* pong = buf + 2 * first;
+    const uint64_t* cur = d_vals;
+    int ext = is_ext;
+    uint32_t left = t, done = 0;
+    while (left > 0) {
+        const uint32_t k = left < 6 ? left : 6;
+        uint64_t* dst = (cur == ping) ? pong : ping;
+        const int rc = fold_device(cur, 1ull << (left - k), k, ext, r + 2 * done, dst, s);
+        if (rc) return rc;
+        cur = dst;
+        ext = 1;
+        left -= k;
+        done += k;
+    }
+    ZK_TRY(hipMemcpyAsync(out, cur, 16, hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    return ZKIE_OK;
+}
+
+// Fold of the listed rows only (the queried-row fold of a STIR round).
+int fold_rows_at_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const uint64_t* ids,
+                        uint64_t n, const uint64_t* r, uint64_t* out, hipStream_t s)
+{
+    if (k > 8 || !r || (n && (!d_mat || !ids || !out))) return ZKIE_ERR_INVALID;
+    if (n == 0) return ZKIE_OK;
+    for (uint64_t i = 0; i < n; i++)
+        if (ids[i] >= h) return ZKIE_ERR_INVALID;
+    const uint64_t width = (is_ext ? 2ull : 1ull) << k;
+    uint64_t* buf = (uint64_t*)workspace(WS_FOLD, (n + n * width + 2 * n) * 8);
+    if (!buf) return ZKIE_ERR_ALLOC;
+    uint64_t* d_ids = buf;
+    uint64_t* d_rows = buf + n;
+    uint64_t* d_out = d_rows + n * width;
+    ZK_TRY(hipMemcpyAsync(d_ids, ids, n * 8, hipMemcpyHostToDevice, s));
+    gather_rows_kernel<<<(unsigned)((n * width + 255) / 256), 256, 0, s>>>(d_mat, width, d_ids, n, d_rows);
+    ZK_LAUNCHED();
+    const int rc = fold_device(d_rows, n, k, is_ext, r, d_out, s);
+    if (rc) return rc;
+    ZK_TRY(hipMemcpyAsync(out, d_out, 2 * n * 8, hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    return ZKIE_OK;
+}
+
 }  // namespace zk
+
+extern "C" int zkie_mle_eval(const uint64_t* d_vals, uint32_t num_vars, int is_ext, const uint64_t* r,
+                             uint64_t* out, void* stream)
+{
+    return zk::mle_eval_device(d_vals, num_vars, is_ext, r, out, zk::as_stream(stream));
+}
+
+extern "C" int zkie_fold_rows_at(const uint64_t* d_mat, uint64_t h, uint32_t log_width, int is_ext,
+                                 const uint64_t* indices, uint64_t n, const uint64_t* r, uint64_t* out,
+                                 void* stream)
+{
+    return zk::fold_rows_at_device(d_mat, h, log_width, is_ext, indices, n, r, out, zk::as_stream(stream));
+}
 
 extern "C" int zkie_fold_rows(const uint64_t* d_mat, uint64_t h, uint32_t log_width, int is_ext,
                               const uint64_t* r, uint64_t* d_out, void* stream)

@@ -207,6 +207,8 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
     if (L > 32) return ZKIE_ERR_INVALID;
     if (w == 0) return ZKIE_OK;
     const uint64_t n = 1ull << L;
+    const Plan p = make_plan(L, w);
+    if (!plan_fits(p, w)) return ZKIE_ERR_INVALID;
     const uint64_t* src = d_in;
     shift = gl_canon(shift);
     if (shift != 1) {
@@ -233,8 +235,6 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
         ZK_TRY(hipStreamSynchronize(s));  // the table buffer is reused by later calls
         src = d_out;
     }
-    const Plan p = make_plan(L, w);
-    if (!plan_fits(p, w)) return ZKIE_ERR_INVALID;
     if (p.np == 1) {
         if (src == d_out) {
             // in place, single pass: rows >= h are treated as zero
@@ -245,6 +245,38 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
     uint64_t* tmp = (uint64_t*)workspace(WS_NTT, n * w * 8);
     if (!tmp) return ZKIE_ERR_ALLOC;
     return run_passes(p, w, src, h, tmp, d_out, false, s);
+}
+
+// Prefix order (writer.rs:43-71): entry (i, j) of the committed matrix, row
+// i < 2^lrows and column j < 2^k, is poly[j 2^lrows + i]; E u64 per entry.
+__global__ __launch_bounds__(256) void prefix_transpose_kernel(const uint64_t* __restrict__ in,
+                                                               uint64_t* __restrict__ out, uint32_t lrows,
+                                                               uint32_t k, uint32_t E)
+{
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (E << (lrows + k))) return;
+    const uint64_t c = t % E, e = t / E;
+    const uint64_t j = e & ((1ull << k) - 1), i = e >> k;
+    out[t] = in[((j << lrows) | i) * E + c];
+}
+
+// commit_extension's encoding (writer.rs:21-86): the 2^n-entry table as a
+// 2^(n-k) x 2^k matrix (Suffix: row-major as stored; Prefix: transposed),
+// zero-padded to 2^log_inv_rate times the height and transformed per column
+// (an EF table transforms per base component, dft_algebra_batch).
+int whir_encode_device(const uint64_t* d_poly, uint32_t n_vars, int is_ext, uint32_t k,
+                       uint32_t log_inv_rate, int prefix, uint64_t* d_out, hipStream_t s)
+{
+    if (k > n_vars || n_vars > 32 || !d_poly || !d_out) return ZKIE_ERR_INVALID;
+    const uint64_t E = is_ext ? 2 : 1;
+    const uint64_t h = 1ull << (n_vars - k), w = E << k;
+    if (!prefix) return lde_device(d_poly, h, w, log_inv_rate, 1, d_out, s);
+    const uint64_t total = h * w;
+    if (d_poly < d_out + total && d_out < d_poly + total) return ZKIE_ERR_INVALID;  // no in-place transpose
+    prefix_transpose_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(d_poly, d_out, n_vars - k, k,
+                                                                          (uint32_t)E);
+    ZK_LAUNCHED();
+    return lde_device(d_out, h, w, log_inv_rate, 1, d_out, s);
 }
 
 }  // namespace zk
@@ -268,6 +300,13 @@ int zkie_dft_batch(uint64_t* d_mat, uint32_t lg_h, uint64_t w, void* stream)
 int zkie_idft_batch(uint64_t* d_mat, uint32_t lg_h, uint64_t w, void* stream)
 {
     return dft_inplace(d_mat, nullptr, lg_h, w, true, as_stream(stream));
+}
+
+int zkie_whir_encode(const uint64_t* d_poly, uint32_t num_vars, int is_ext, uint32_t log_width,
+                     uint32_t log_inv_rate, int prefix, uint64_t* d_out, void* stream)
+{
+    return whir_encode_device(d_poly, num_vars, is_ext, log_width, log_inv_rate, prefix, d_out,
+                              as_stream(stream));
 }
 
 int zkie_lde_batch(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,

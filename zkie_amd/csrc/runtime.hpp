@@ -27,7 +27,7 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Grow-only device scratch, one per (device, slot); the same role as the
 // reference's CudaBuffer arenas (cuda_buffer.rs:7-57). Returns nullptr on
 // allocation failure. Not thread-safe across host threads sharing a device.
-enum WorkspaceSlot { WS_NTT = 0, WS_MERKLE = 1, WS_MISC = 2, WS_COUNT = 3 };
+enum WorkspaceSlot { WS_NTT = 0, WS_MERKLE = 1, WS_MISC = 2, WS_FOLD = 3, WS_COUNT = 4 };
 void* workspace(WorkspaceSlot slot, size_t bytes);
 
 // Kernel timers: when profiling is on, every instrumented launch records a

@@ -7,7 +7,10 @@ Mirrors the engines of the reference's WHIR wrapper:
                          Mmcs::{commit, open_batch, open_multi_batch};
   * HipMerkleTree     <- the MerkleTree prover data (p3-merkle-tree
                          merkle_tree.rs:32-70), kept device-resident;
-  * fold_rows         <- the WHIR row fold (p3-whir prover/mod.rs:257-290).
+  * fold_rows         <- the WHIR row fold (p3-whir prover/mod.rs:257-290);
+    fold_rows_at      <- its queried-row form (prover/mod.rs:265-290);
+  * mle_eval          <- the OOD answer sumcheck_prover.eval (prover/mod.rs:226-236);
+  * whir_encode       <- commit_extension's encoding (committer/writer.rs:21-86).
 Unlike the reference there is no CPU fallback: every failure raises.
 """
 from __future__ import annotations
@@ -159,3 +162,31 @@ def fold_rows(mat, k: int, r, is_ext: bool) -> np.ndarray:
     out = DeviceBuffer(2 * h)
     fold_rows_device(d, h, k, r, is_ext, out)
     return out.download().reshape(h, 2)
+
+
+def fold_rows_at(d_mat: DeviceBuffer, h: int, k: int, is_ext: bool, indices, r, stream=None) -> np.ndarray:
+    """Fold of the rows `indices` of a device matrix only (n x 2 EF, host)."""
+    idx = np.ascontiguousarray(np.asarray(indices, np.uint64).reshape(-1))
+    rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
+    assert rr.size == 2 * k
+    out = np.zeros(2 * idx.size, np.uint64)
+    check(N.load().zkie_fold_rows_at(d_mat.addr, h, k, 1 if is_ext else 0, N.p(idx), idx.size, N.p(rr),
+                                     N.p(out), stream), "zkie_fold_rows_at")
+    return out.reshape(-1, 2)
+
+
+def mle_eval(d_vals: DeviceBuffer, num_vars: int, is_ext: bool, r, stream=None) -> np.ndarray:
+    """sum_j eq(r, j) v[j] over a device table of 2^num_vars entries (EF, host)."""
+    rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
+    assert rr.size == 2 * num_vars
+    out = np.zeros(2, np.uint64)
+    check(N.load().zkie_mle_eval(d_vals.addr, num_vars, 1 if is_ext else 0, N.p(rr), N.p(out), stream),
+          "zkie_mle_eval")
+    return out
+
+
+def whir_encode(d_poly: DeviceBuffer, num_vars: int, is_ext: bool, log_width: int, log_inv_rate: int,
+                prefix: bool, d_out: DeviceBuffer, stream=None):
+    """commit_extension's codeword of a device table into d_out (row-major)."""
+    check(N.load().zkie_whir_encode(d_poly.addr, num_vars, 1 if is_ext else 0, log_width, log_inv_rate,
+                                    1 if prefix else 0, d_out.addr, stream), "zkie_whir_encode")
