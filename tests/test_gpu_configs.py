@@ -140,3 +140,39 @@ def test_workload_full_size_properties(native, oracle, number):
     d_in = DeviceBuffer.from_array(data)
     out = PL.run_workload(wl, d_in, with_openings=False)
     property_checks(native, oracle, wl, data, out, np.random.default_rng(number))
+
+
+@pytest.mark.gpu
+def test_whir_rounds_ood_and_stir_full_size(native, oracle):
+    """The WHIR-shaped workload at full size: every round's out-of-domain
+    answers equal the oracle's multilinear evaluation of the folded table,
+    the STIR row folds equal the oracle's fold of the opened rows, and each
+    row fold agrees with the next codeword (FRI/STIR consistency): the fold
+    of row t of a codeword with N rows is sum_c w_N^(c t) C'[t mod N/2^k][c]."""
+    wl = C.CONFIGS[5]
+    print("CASE whir rounds OOD + STIR", wl.name, flush=True)
+    k = wl.fold_k
+    out = PL.run_workload(wl, DeviceBuffer.from_array(PL.workload_inputs(wl)), with_openings=False)
+    assert len(out.rounds) == wl.rounds + 1
+    for r in range(1, len(out.rounds)):
+        prev, rnd = out.rounds[r - 1], out.rounds[r]
+        table, t_entries = out.tables[r - 1]
+        tab = table.download()
+        n_vars = t_entries.bit_length() - 1
+        for z, ans in zip(rnd.ood_points, rnd.ood_answers):
+            assert (ans == oracle.mle_eval(tab, C.ef_pow2_chain(z, n_vars), True)).all()
+        idx = rnd.stir_indices.astype(np.int64)
+        prev_cw = prev.codeword.download().reshape(prev.rows, prev.width)
+        ch = C.challenges(k * wl.rounds)[k * (r - 1):k * r]
+        assert (rnd.stir_folds == oracle.fold_rows(prev_cw[idx], k, ch, r > 1)).all()
+        # consistency with the next codeword (EF rows of 2^k entries)
+        N, M = prev.rows, rnd.rows
+        cw = rnd.codeword.download().reshape(M, 1 << k, 2)
+        w_n = pow(7, (C.P - 1) // N, C.P)
+        for t, f in zip(idx[:16], rnd.stir_folds[:16]):
+            acc0 = acc1 = 0
+            for c in range(1 << k):
+                wc = pow(w_n, int(c * t), C.P)
+                acc0 = (acc0 + wc * int(cw[t % M, c, 0])) % C.P
+                acc1 = (acc1 + wc * int(cw[t % M, c, 1])) % C.P
+            assert [acc0, acc1] == [int(f[0]), int(f[1])]

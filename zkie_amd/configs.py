@@ -1,6 +1,6 @@
 """The synthetic commitment workloads (shapes, generators, seeds).
 
-Seeds: data 0, fold challenges 1, query indices 2. Inputs come from the
+Seeds: data 0, fold challenges 1, query indices 2, out-of-domain points 3. Inputs come from the
 XorShift64 generator of common/field.rs:17-36 (zkie_gen_inputs).
   1  2^16 int16 values, one column, blowup 4 -> 2^18-row codeword, Merkle root.
   2  GPT-2-small 768x3072 weight matrix, Irwin-Hall gaussian int16
@@ -23,7 +23,7 @@ from dataclasses import dataclass
 import numpy as np
 
 GEN_UNIFORM, GEN_I16, GEN_I8, GEN_GAUSS_I16 = 0, 1, 2, 3
-SEED_DATA, SEED_CHALLENGES, SEED_QUERIES = 0, 1, 2
+SEED_DATA, SEED_CHALLENGES, SEED_QUERIES, SEED_OOD = 0, 1, 2, 3
 P = 0xFFFFFFFF00000001
 
 
@@ -87,6 +87,19 @@ def challenges(count: int, seed: int = SEED_CHALLENGES) -> np.ndarray:
     """`count` EF challenges (c0, c1), each c = field() (uniform mod p)."""
     g = XorShift64(seed)
     return np.array([[g.field(), g.field()] for _ in range(count)], np.uint64)
+
+
+def ef_pow2_chain(z, n: int) -> np.ndarray:
+    """[z, z^2, z^4, ..., z^(2^(n-1))] in EF = F[x]/(x^2 - 7): the coordinates
+    of a univariate out-of-domain sample z expanded to n variables, variable 0
+    first (p3's Point::expand_from_univariate lists the same powers most
+    significant variable first; zkie_mle_eval takes variable 0 first)."""
+    out = []
+    c0, c1 = int(z[0]) % P, int(z[1]) % P
+    for _ in range(n):
+        out.append([c0, c1])
+        c0, c1 = (c0 * c0 + 7 * c1 * c1) % P, (2 * c0 * c1) % P
+    return np.array(out, np.uint64).reshape(n, 2)
 
 
 def query_indices(count: int, height: int, g: XorShift64) -> np.ndarray:

@@ -6,6 +6,11 @@ commit_round  <- one WHIR round's encode + commit: p3-whir
                  dft_batch per column, Merkle commit of the codeword rows)
 fold          <- the row fold of p3-whir src/pcs/prover/mod.rs:257-290 and the
                  table fold over the low k variables (common/mle.rs:25-38)
+round loop    <- WhirProver::round (prover/mod.rs:196-300) with seeded
+                 challenges: fold the table, encode + commit it, answer
+                 out-of-domain samples on the new table (mod.rs:226-236), then
+                 open the previous codeword at STIR indices and fold the opened
+                 rows with the round's challenges (mod.rs:247-290)
 run_workload  <- the five workloads of zkie_amd.configs, everything in HBM;
                  only roots, requested openings and checks leave the device.
 """
@@ -16,9 +21,10 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _native as N
-from .configs import (SEED_CHALLENGES, SEED_DATA, SEED_QUERIES, Workload, XorShift64,
-                      challenges, query_indices)
-from .pcs import HipMerkleTree, HipMerkleTreeMmcs, fold_rows_device, lde_device
+from .configs import (SEED_CHALLENGES, SEED_DATA, SEED_OOD, SEED_QUERIES, Workload, XorShift64,
+                      challenges, ef_pow2_chain, query_indices)
+from .pcs import (HipMerkleTree, HipMerkleTreeMmcs, fold_rows_at, fold_rows_device, lde_device,
+                  mle_eval)
 from ._native import DeviceBuffer
 
 
@@ -32,6 +38,10 @@ class RoundOutput:
     opened_rows: np.ndarray | None = None
     paths: np.ndarray | None = None
     pruned: np.ndarray | None = None
+    ood_points: list = field(default_factory=list)   # EF z of each out-of-domain sample
+    ood_answers: list = field(default_factory=list)  # table evaluations at z^(2^i)
+    stir_indices: np.ndarray | None = None  # rows of the previous codeword opened this round
+    stir_folds: np.ndarray | None = None    # their row folds with this round's challenges
 
 
 @dataclass
@@ -80,14 +90,26 @@ def run_workload(wl: Workload, d_in: DeviceBuffer, with_openings: bool = True,
         fold_rows_device(r0.codeword, r0.rows, k, ch, False, out.fold, stream=stream)
     if wl.rounds:
         ch = challenges(k * wl.rounds)
+        g_ood, g_stir = XorShift64(SEED_OOD), XorShift64(SEED_QUERIES + 100)
         table, t_rows, ext = d_in, wl.rows, False
         for r in range(wl.rounds):
+            chr_ = ch[k * r:k * (r + 1)]
             folded = DeviceBuffer(2 * t_rows)
-            fold_rows_device(table, t_rows, k, ch[k * r:k * (r + 1)], ext, folded, stream=stream)
+            fold_rows_device(table, t_rows, k, chr_, ext, folded, stream=stream)
             out.tables.append((folded, t_rows))
+            prev = out.rounds[-1]
             table, ext = folded, True
+            n_vars = (t_rows.bit_length() - 1)  # the folded table holds t_rows EF entries
             t_rows = t_rows >> k  # EF table of t_rows entries -> rows of 2^k EF
             rnd = commit_round(folded, t_rows, 2 << k, wl.log_blowup, mmcs, stream=stream)
+            for _ in range(2):
+                z = np.array([g_ood.field(), g_ood.field()], np.uint64)
+                rnd.ood_points.append(z)
+                rnd.ood_answers.append(mle_eval(folded, n_vars, True, ef_pow2_chain(z, n_vars), stream))
+            if wl.queries:
+                rnd.stir_indices = query_indices(wl.queries, prev.rows, g_stir)
+                rnd.stir_folds = fold_rows_at(prev.codeword, prev.rows, k, r > 0, rnd.stir_indices, chr_,
+                                              stream)
             out.rounds.append(rnd)
     if with_openings and wl.queries:
         g = XorShift64(SEED_QUERIES)
