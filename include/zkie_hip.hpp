@@ -1,0 +1,248 @@
+/* C++ host interface over the C ABI of libzkie_hip.so (header only).
+ *
+ * Mirrors the engines zkIE plugs into its WHIR PCS (crates/zkie-core/src/pcs):
+ *   zkie::HipDft             <- CudaDft, TwoAdicSubgroupDft<Goldilocks>
+ *                               (dft_cuda.rs:122-222): dft_batch over
+ *                               row-major matrices, natural order in and out;
+ *   zkie::HipMerkleTreeMmcs  <- CudaMerkleTreeMmcs, Mmcs<F> (merkle_cuda.rs:
+ *                               315-395): commit, open_batch, open_multi_batch;
+ *   zkie::MerkleTree         <- the MerkleTree prover data (p3-merkle-tree
+ *                               merkle_tree.rs:32-70), kept in device memory;
+ *   zkie::fold_rows, zkie::mle_eval <- the WHIR row fold and out-of-domain
+ *                               evaluation (p3-whir prover/mod.rs:226-290).
+ * Matrices are p3's RowMajorMatrix<F> (values row-major, canonical u64).
+ * Errors: every non-zero status of the C ABI throws zkie::Error carrying it;
+ * there is no CPU fallback here (the reference's Rust caller keeps its own,
+ * dft_cuda.rs:174-177). Calls on one device are serialised by the caller. */
+#pragma once
+
+#include <array>
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "zkie_hip.h"
+
+namespace zkie {
+
+using F = uint64_t;
+using Digest = std::array<F, 8>;  // [F; DIGEST_ELEMS]
+using Ef = std::array<F, 2>;      // BinomialExtensionField<F, 2>, [c0, c1]
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int rc, const std::string& what)
+        : std::runtime_error(what + " failed with status " + std::to_string(rc)), code(rc)
+    {
+    }
+};
+
+inline void check(int rc, const char* what)
+{
+    if (rc != 0) throw Error(rc, what);
+}
+
+/* The EF coordinates of a possibly empty point, as the ABI's pointer. */
+inline const F* ef_ptr(const std::vector<std::array<F, 2>>& r)
+{
+    static const F none[2] = {0, 0};
+    return r.empty() ? none : r[0].data();
+}
+
+struct RowMajorMatrix {
+    std::vector<F> values;
+    size_t width = 0;
+    size_t height() const { return width ? values.size() / width : 0; }
+    const F* row(size_t r) const { return values.data() + r * width; }
+};
+
+/* Device allocation owned by this object (the CudaBuffer role of cuda_buffer.rs). */
+class DeviceBuffer {
+   public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t elems) : n_(elems)
+    {
+        check(zkie_dev_alloc(&ptr_, (elems ? elems : 1) * sizeof(F)), "zkie_dev_alloc");
+    }
+    static DeviceBuffer upload(const std::vector<F>& v)
+    {
+        DeviceBuffer b(v.size());
+        if (!v.empty()) check(zkie_memcpy_htod(b.ptr_, v.data(), v.size() * sizeof(F)), "zkie_memcpy_htod");
+        return b;
+    }
+    std::vector<F> download() const
+    {
+        std::vector<F> v(n_);
+        if (n_) check(zkie_memcpy_dtoh(v.data(), ptr_, n_ * sizeof(F)), "zkie_memcpy_dtoh");
+        return v;
+    }
+    DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), n_(o.n_) { o.ptr_ = nullptr, o.n_ = 0; }
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept
+    {
+        std::swap(ptr_, o.ptr_);
+        std::swap(n_, o.n_);
+        return *this;
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer()
+    {
+        if (ptr_) (void)zkie_dev_free(ptr_);
+    }
+    F* data() const { return static_cast<F*>(ptr_); }
+    size_t size() const { return n_; }
+
+   private:
+    void* ptr_ = nullptr;
+    size_t n_ = 0;
+};
+
+inline uint32_t log2_exact(size_t n, const char* what)
+{
+    uint32_t lg = 0;
+    while ((size_t(1) << lg) < n) lg++;
+    if ((size_t(1) << lg) != n) throw Error(ZKIE_ERR_INVALID, what);
+    return lg;
+}
+
+/* TwoAdicSubgroupDft<Goldilocks> (dft_cuda.rs:161-222). */
+class HipDft {
+   public:
+    /* out[i][c] = sum_j in[j][c] w_h^(ij), w_h = TWO_ADIC_GENERATORS[log h]. */
+    RowMajorMatrix dft_batch(RowMajorMatrix mat) const { return run(std::move(mat), false); }
+    /* The inverse transform, including the 1/h scale. */
+    RowMajorMatrix idft_batch(RowMajorMatrix mat) const { return run(std::move(mat), true); }
+    /* Coefficients zero-padded to height << added_bits, optionally scaled by
+     * shift^i, then dft_batch: the encoding of commit_extension (writer.rs:21-86). */
+    RowMajorMatrix lde_batch(const RowMajorMatrix& coeffs, uint32_t added_bits, F shift = 1) const
+    {
+        const size_t h = coeffs.height(), w = coeffs.width;
+        (void)log2_exact(h, "lde_batch height");
+        DeviceBuffer in = DeviceBuffer::upload(coeffs.values), out((h << added_bits) * w);
+        check(zkie_lde_batch(in.data(), h, w, added_bits, shift, out.data(), nullptr), "zkie_lde_batch");
+        return RowMajorMatrix{out.download(), w};
+    }
+
+   private:
+    static RowMajorMatrix run(RowMajorMatrix mat, bool inverse)
+    {
+        const size_t h = mat.height(), w = mat.width;
+        if (h <= 1) return mat;  // dft_cuda.rs:164-166
+        const uint32_t lg = log2_exact(h, "dft_batch height");
+        DeviceBuffer d = DeviceBuffer::upload(mat.values);
+        check(inverse ? zkie_idft_batch(d.data(), lg, w, nullptr) : zkie_dft_batch(d.data(), lg, w, nullptr),
+              inverse ? "zkie_idft_batch" : "zkie_dft_batch");
+        mat.values = d.download();
+        return mat;
+    }
+};
+
+/* MerkleTree prover data (merkle_tree.rs:32-70), device resident. */
+struct MerkleTree {
+    DeviceBuffer mat;
+    size_t height = 0, width = 0;
+    DeviceBuffer layers;
+    std::vector<uint64_t> layer_lens;  // digests per layer, leaves first
+    Digest root{};
+};
+
+using MerkleCap = std::vector<Digest>;  // cap height 0: the root
+
+/* BatchOpening (p3-commit): one opened row per matrix, the sibling path bottom-up. */
+struct BatchOpening {
+    std::vector<std::vector<F>> opened_values;
+    std::vector<Digest> opening_proof;
+};
+
+/* PrunedMerklePaths (pruning.rs:83-89), as the frontier-ordered sibling list. */
+struct PrunedMerklePaths {
+    std::vector<Digest> digests;
+};
+
+/* Mmcs<F> with MerkleTree<F, F, M, 2, 8> prover data (merkle_cuda.rs:315-395). */
+class HipMerkleTreeMmcs {
+   public:
+    /* One matrix per commitment (WHIR commits one, p3-whir pcs/proof.rs:114-121). */
+    std::pair<MerkleCap, MerkleTree> commit(const RowMajorMatrix& m) const
+    {
+        MerkleTree t;
+        t.height = m.height();
+        t.width = m.width;
+        uint32_t nl = 0;
+        std::vector<uint64_t> lens(65);
+        check(zkie_merkle_layout(t.height, &nl, lens.data()), "zkie_merkle_layout");
+        lens.resize(nl);
+        size_t total = 0;
+        for (uint64_t l : lens) total += l;
+        t.layer_lens = lens;
+        t.mat = DeviceBuffer::upload(m.values);
+        t.layers = DeviceBuffer(total * 8);
+        check(zkie_merkle_commit(t.mat.data(), t.height, t.width, t.layers.data(), t.root.data(), nullptr),
+              "zkie_merkle_commit");
+        MerkleCap cap{t.root};
+        return {std::move(cap), std::move(t)};
+    }
+
+    /* mmcs/batch.rs:75-121. */
+    BatchOpening open_batch(size_t index, const MerkleTree& t) const
+    {
+        const uint64_t idx = index;
+        BatchOpening o;
+        o.opened_values.assign(1, std::vector<F>(t.width));
+        o.opening_proof.resize(t.layer_lens.size() - 1);
+        check(zkie_merkle_open_batch(t.mat.data(), t.height, t.width, t.layers.data(), &idx, 1,
+                                     o.opened_values[0].data(), o.opening_proof.empty() ? nullptr : o.opening_proof[0].data(),
+                                     nullptr),
+              "zkie_merkle_open_batch");
+        return o;
+    }
+
+    /* mmcs/mod.rs:309-461: opened rows per index (one matrix each) and the pruned proof. */
+    std::pair<std::vector<std::vector<std::vector<F>>>, PrunedMerklePaths> open_multi_batch(
+        const std::vector<size_t>& indices, const MerkleTree& t) const
+    {
+        std::vector<uint64_t> idx(indices.begin(), indices.end());
+        std::vector<F> rows(idx.size() * t.width);
+        // a pruned proof holds at most one sibling per index per level
+        const uint64_t cap = (uint64_t)idx.size() * (t.layer_lens.size() - 1) + 1;
+        std::vector<Digest> pruned(cap);
+        uint64_t count = 0;
+        check(zkie_merkle_open_pruned(t.mat.data(), t.height, t.width, t.layers.data(), idx.data(), idx.size(),
+                                      rows.data(), pruned[0].data(), cap, &count, nullptr),
+              "zkie_merkle_open_pruned");
+        pruned.resize(count);
+        std::vector<std::vector<std::vector<F>>> opened(idx.size());
+        for (size_t i = 0; i < idx.size(); i++)
+            opened[i].emplace_back(rows.begin() + i * t.width, rows.begin() + (i + 1) * t.width);
+        return {std::move(opened), PrunedMerklePaths{std::move(pruned)}};
+    }
+};
+
+/* Row fold (prover/mod.rs:257-290; mle.rs:8-22 with variable 0 the least
+ * significant bit) of every row of a device matrix of 2^k (EF: 2^(k+1)) u64 per row. */
+inline std::vector<Ef> fold_rows(const DeviceBuffer& d_mat, size_t h, uint32_t k, bool is_ext,
+                                 const std::vector<Ef>& r)
+{
+    if (r.size() != k) throw Error(ZKIE_ERR_INVALID, "fold_rows challenges");
+    DeviceBuffer out(2 * h);
+    check(zkie_fold_rows(d_mat.data(), h, k, is_ext ? 1 : 0, ef_ptr(r), out.data(), nullptr),
+          "zkie_fold_rows");
+    const std::vector<F> v = out.download();
+    std::vector<Ef> res(h);
+    for (size_t i = 0; i < h; i++) res[i] = {v[2 * i], v[2 * i + 1]};
+    return res;
+}
+
+/* Out-of-domain answer: the multilinear extension of a device table at r. */
+inline Ef mle_eval(const DeviceBuffer& d_vals, uint32_t num_vars, bool is_ext, const std::vector<Ef>& r)
+{
+    if (r.size() != num_vars) throw Error(ZKIE_ERR_INVALID, "mle_eval point");
+    Ef out{};
+    check(zkie_mle_eval(d_vals.data(), num_vars, is_ext ? 1 : 0, ef_ptr(r), out.data(), nullptr), "zkie_mle_eval");
+    return out;
+}
+
+}  // namespace zkie

@@ -1,0 +1,121 @@
+// Parity test of the C++ host interface (include/zkie_hip.hpp) against the
+// oracle, written like the reference's own engine tests: transform and
+// inverse round trip, encode, commit, open, verify, pruned multi-opening,
+// fold, and the error path. Needs a HIP device; prints one line per check and
+// exits non-zero on the first mismatch.
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "zkie_hip.hpp"
+
+extern "C" {
+#include "zkie_oracle.h"
+}
+
+using zkie::F;
+
+static int g_checks = 0;
+#define EXPECT(cond, what)                                                   \
+    do {                                                                     \
+        if (!(cond)) {                                                       \
+            std::printf("FAIL %s (line %d)\n", what, __LINE__);              \
+            std::exit(1);                                                    \
+        }                                                                    \
+        std::printf("ok   %s\n", what);                                      \
+        std::fflush(stdout);                                                 \
+        g_checks++;                                                          \
+    } while (0)
+
+static zkie::RowMajorMatrix random_matrix(uint64_t seed, size_t h, size_t w)
+{
+    zkie::RowMajorMatrix m{std::vector<F>(h * w), w};
+    or_gen_uniform(seed, h * w, m.values.data());
+    return m;
+}
+
+int main()
+{
+    or_set_threads(4);
+    std::printf("CASE C++ host interface\n");
+    std::fflush(stdout);
+    if (zkie_device_count() < 1) {
+        std::printf("FAIL no HIP device\n");
+        return 1;
+    }
+    zkie::HipDft dft;
+    zkie::HipMerkleTreeMmcs mmcs;
+
+    // dft_batch / idft_batch
+    const auto m = random_matrix(1, 1 << 10, 8);
+    const auto ev = dft.dft_batch(m);
+    std::vector<F> ref = m.values;
+    or_dft_batch(ref.data(), 10, 8);
+    EXPECT(ev.values == ref, "dft_batch 2^10 x 8 equals the oracle");
+    EXPECT(dft.idft_batch(ev).values == m.values, "idft_batch inverts dft_batch");
+    EXPECT(dft.dft_batch(random_matrix(2, 1, 5)).values == random_matrix(2, 1, 5).values,
+           "dft_batch of one row is the identity");
+
+    // lde_batch (commit_extension's encoding)
+    const auto c = random_matrix(3, 1 << 9, 16);
+    const auto cw = dft.lde_batch(c, 2);
+    std::vector<F> cw_ref((size_t(1) << 11) * 16);
+    or_lde_batch(c.values.data(), 1 << 9, 16, 2, 1, cw_ref.data());
+    EXPECT(cw.values == cw_ref && cw.height() == (1u << 11), "lde_batch blowup 4 equals the oracle");
+
+    // commit / open_batch / verify
+    const size_t h = cw.height();
+    auto [cap, tree] = mmcs.commit(cw);
+    std::vector<F> layers_ref(8 * (2 * h));
+    zkie::Digest root_ref{};
+    or_merkle_commit(cw.values.data(), h, 16, layers_ref.data(), root_ref.data());
+    EXPECT(cap.size() == 1 && cap[0] == root_ref, "commit root equals the oracle");
+    for (size_t idx : {size_t(0), size_t(1), size_t(777), h - 1}) {
+        const auto o = mmcs.open_batch(idx, tree);
+        std::vector<F> sib(8 * (tree.layer_lens.size() - 1));
+        or_merkle_open(layers_ref.data(), h, idx, sib.data());
+        bool same = o.opened_values[0] == std::vector<F>(cw.row(idx), cw.row(idx) + 16);
+        for (size_t l = 0; l < o.opening_proof.size(); l++)
+            for (int e = 0; e < 8; e++) same = same && o.opening_proof[l][e] == sib[8 * l + e];
+        EXPECT(same, "open_batch row and path equal the oracle");
+        EXPECT(or_merkle_verify(cap[0].data(), h, idx, o.opened_values[0].data(), 16,
+                                o.opening_proof[0].data()) == 1,
+               "open_batch verifies against the root");
+    }
+
+    // open_multi_batch (pruned)
+    const std::vector<size_t> q = {3, 4, 100, 1024, 2047};
+    auto [rows, pruned] = mmcs.open_multi_batch(q, tree);
+    std::vector<uint64_t> qi(q.begin(), q.end());
+    std::vector<F> pref(8 * q.size() * 16);
+    const uint64_t n = or_merkle_open_pruned(layers_ref.data(), h, qi.data(), qi.size(), pref.data(),
+                                             q.size() * 16);
+    bool same = pruned.digests.size() == n;
+    for (size_t i = 0; same && i < n; i++)
+        for (int e = 0; e < 8; e++) same = same && pruned.digests[i][e] == pref[8 * i + e];
+    for (size_t i = 0; i < q.size(); i++)
+        same = same && rows[i][0] == std::vector<F>(cw.row(q[i]), cw.row(q[i]) + 16);
+    EXPECT(same, "open_multi_batch rows and pruned proof equal the oracle");
+
+    // fold of the committed codeword
+    std::vector<zkie::Ef> r(4);
+    for (int b = 0; b < 4; b++) r[b] = {F(1000 + b), F(7 * b + 1)};
+    const auto f = zkie::fold_rows(tree.mat, h, 4, false, r);
+    std::vector<F> fref(2 * h);
+    or_fold_rows(cw.values.data(), h, 4, 0, &r[0][0], fref.data());
+    same = true;
+    for (size_t i = 0; i < h; i++) same = same && f[i][0] == fref[2 * i] && f[i][1] == fref[2 * i + 1];
+    EXPECT(same, "fold_rows equals the oracle");
+
+    // error path: an index outside the tree is a status, thrown as zkie::Error
+    bool threw = false;
+    try {
+        (void)mmcs.open_batch(h, tree);
+    } catch (const zkie::Error& e) {
+        threw = e.code == ZKIE_ERR_INVALID;
+    }
+    EXPECT(threw, "open_batch past the last row throws zkie::Error(ZKIE_ERR_INVALID)");
+
+    std::printf("ALL PASS %d\n", g_checks);
+    return 0;
+}
