@@ -103,12 +103,13 @@ def main():
     L = N.load()
     import numpy as np
     root = np.zeros(8, np.uint64)
+    stream = N.Stream()
 
     def step():
-        lde_device(d_in, wl.rows, w, wl.log_blowup, d_cw)
-        N.check(L.zkie_merkle_commit(d_cw.addr, n, w, d_layers.addr, N.p(root), None), "commit")
+        lde_device(d_in, wl.rows, w, wl.log_blowup, d_cw, stream=stream.handle)
+        N.check(L.zkie_merkle_commit(d_cw.addr, n, w, d_layers.addr, N.p(root), stream.handle), "commit")
         if wl.fold_k:
-            fold_rows_device(d_cw, n, wl.fold_k, ch, False, d_fold)
+            fold_rows_device(d_cw, n, wl.fold_k, ch, False, d_fold, stream=stream.handle)
 
     for _ in range(args.warmup):
         step()

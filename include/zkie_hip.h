@@ -48,6 +48,14 @@ int zkie_memcpy_dtod(void *d_dst, const void *d_src, size_t bytes, void *stream)
 int zkie_memset(void *d_ptr, int value, size_t bytes);
 int zkie_device_synchronize(void);
 int zkie_stream_synchronize(void *stream);
+/* Streams for overlapping independent stages (no reference counterpart: the
+ * reference runs everything on the legacy default stream, merkle_cuda.rs:282).
+ * zkie_stream_create makes a non-blocking stream of the default priority;
+ * zkie_stream_wait makes work queued on `waiter` afterwards wait for the work
+ * queued on `signaler` so far. */
+int zkie_stream_create(void **stream);
+int zkie_stream_destroy(void *stream);
+int zkie_stream_wait(void *waiter, void *signaler);
 
 /* ------------------------------------------------------------------------
  * Reference-compatible kernels (same names, arguments and semantics as

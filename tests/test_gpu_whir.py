@@ -78,3 +78,24 @@ def test_whir_encode_prefix_rejects_overlap(native, oracle):
     buf = DeviceBuffer(1 << 12)
     rc = N.load().zkie_whir_encode(buf.addr, 8, 0, 2, 2, 1, buf.addr, None)
     assert rc == -1
+
+
+def test_streams_order_dependent_work(native, oracle):
+    """A fold queued on a second stream after zkie_stream_wait sees the LDE
+    queued before it on the first stream (the stream plumbing of the ABI)."""
+    from zkie_amd import _native as N
+    from zkie_amd import pcs
+    from zkie_amd._native import DeviceBuffer
+
+    print("CASE streams", flush=True)
+    h, w, lb = 1 << 12, 16, 2
+    data = oracle.gen_uniform(77, h * w).reshape(h, w)
+    d_in, d_cw, d_f = DeviceBuffer.from_array(data), DeviceBuffer(h * w << lb), DeviceBuffer(2 * (h << lb))
+    a, b = N.Stream(), N.Stream()
+    r = _r(oracle, 78, 4)
+    pcs.lde_device(d_in, h, w, lb, d_cw, stream=a.handle)
+    b.wait(a)
+    pcs.fold_rows_device(d_cw, h << lb, 4, r, False, d_f, stream=b.handle)
+    b.synchronize()
+    want = oracle.fold_rows(oracle.lde_batch(data, lb), 4, r, False)
+    assert (d_f.download().reshape(-1, 2) == want).all()

@@ -29,6 +29,9 @@ SIGNATURES = {
     "zkie_memset": [_vp, _int, _sz],
     "zkie_device_synchronize": [],
     "zkie_stream_synchronize": [_vp],
+    "zkie_stream_create": [ctypes.POINTER(_vp)],
+    "zkie_stream_destroy": [_vp],
+    "zkie_stream_wait": [_vp, _vp],
     "zkie_ntt_forward_goldilocks": [_vp, _vp, _u32, _u64, _vp],
     "zkie_p2_upload_constants": [_u64p, _u64p, _u64p, _u64],
     "zkie_p2_leaf_batch": [_vp, _vp, _u32, _u32],
@@ -180,3 +183,27 @@ def profile_names():
     buf = ctypes.create_string_buffer(1 << 16)
     check(load().zkie_profile_names(buf, len(buf)), "zkie_profile_names")
     return [x for x in buf.value.decode().split("\n") if x]
+
+
+class Stream:
+    """A non-blocking HIP stream of the default priority owned by this object."""
+
+    def __init__(self):
+        self.ptr = _vp()
+        check(load().zkie_stream_create(ctypes.byref(self.ptr)), "zkie_stream_create")
+
+    @property
+    def handle(self):
+        return self.ptr.value
+
+    def wait(self, other: "Stream") -> None:
+        """Later work on self waits for the work queued on `other` so far."""
+        check(load().zkie_stream_wait(self.handle, other.handle), "zkie_stream_wait")
+
+    def synchronize(self) -> None:
+        check(load().zkie_stream_synchronize(self.handle), "zkie_stream_synchronize")
+
+    def __del__(self):
+        if getattr(self, "ptr", None) is not None and self.ptr.value:
+            load().zkie_stream_destroy(self.ptr)
+            self.ptr = _vp()

@@ -17,11 +17,19 @@
 namespace zk {
 namespace {
 
+// eq weights of a fold with k <= 6 (at most 64 EF values), passed by value
+// as a kernel argument: they reach the kernel as scalar loads from the
+// argument segment, and no device buffer has to outlive the launch, so the
+// call does not synchronise its stream.
+struct EqArg {
+    uint64_t v[128];
+};
+
 template <int K, bool EXT>
 __global__ __launch_bounds__(256) void fold_kernel(const uint64_t* __restrict__ mat, uint64_t h,
-                                                   const uint64_t* __restrict__ eq,
-                                                   uint64_t* __restrict__ out)
+                                                   const EqArg eqa, uint64_t* __restrict__ out)
 {
+    const uint64_t* eq = eqa.v;
     constexpr int Wd = 1 << K;
     constexpr int RW = EXT ? 2 * Wd : Wd;  // u64 per row
     const uint64_t* row;
@@ -114,33 +122,40 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
     if (k > 8 || !r || (h && (!d_mat || !d_out))) return ZKIE_ERR_INVALID;
     if (h == 0) return ZKIE_OK;
     const std::vector<uint64_t> eq = eq_table(r, k);
-    uint64_t* d_eq = (uint64_t*)workspace(WS_MISC, eq.size() * 8);
-    if (!d_eq) return ZKIE_ERR_ALLOC;
-    ZK_TRY(hipMemcpyAsync(d_eq, eq.data(), eq.size() * 8, hipMemcpyHostToDevice, s));
     const unsigned grid = (unsigned)((h + 255) / 256);
-    ProfMark m = prof_begin("fold_rows", s);
+    if (k <= 6) {
+        EqArg ea{};
+        for (size_t i = 0; i < eq.size(); i++) ea.v[i] = eq[i];
+        ProfMark m = prof_begin("fold_rows", s);
 #define ZK_FOLD(KK)                                                                  \
     case KK:                                                                         \
         if (is_ext)                                                                  \
-            fold_kernel<KK, true><<<grid, 256, 0, s>>>(d_mat, h, d_eq, d_out);       \
+            fold_kernel<KK, true><<<grid, 256, 0, s>>>(d_mat, h, ea, d_out);         \
         else                                                                         \
-            fold_kernel<KK, false><<<grid, 256, 0, s>>>(d_mat, h, d_eq, d_out);      \
+            fold_kernel<KK, false><<<grid, 256, 0, s>>>(d_mat, h, ea, d_out);        \
         break;
-    switch (k) {
-        ZK_FOLD(1)
-        ZK_FOLD(2)
-        ZK_FOLD(3)
-        ZK_FOLD(4)
-        ZK_FOLD(5)
-        ZK_FOLD(6)
-        default:
-            if (is_ext)
-                fold_kernel_rt<true><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
-            else
-                fold_kernel_rt<false><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
-            break;
-    }
+        switch (k) {
+            ZK_FOLD(0)
+            ZK_FOLD(1)
+            ZK_FOLD(2)
+            ZK_FOLD(3)
+            ZK_FOLD(4)
+            ZK_FOLD(5)
+            default: ZK_FOLD(6)
+        }
 #undef ZK_FOLD
+        prof_end(m, s);
+        ZK_LAUNCHED();
+        return ZKIE_OK;
+    }
+    uint64_t* d_eq = (uint64_t*)workspace(WS_MISC, eq.size() * 8);
+    if (!d_eq) return ZKIE_ERR_ALLOC;
+    ZK_TRY(hipMemcpyAsync(d_eq, eq.data(), eq.size() * 8, hipMemcpyHostToDevice, s));
+    ProfMark m = prof_begin("fold_rows", s);
+    if (is_ext)
+        fold_kernel_rt<true><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
+    else
+        fold_kernel_rt<false><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
     prof_end(m, s);
     ZK_LAUNCHED();
     // The eq buffer is shared workspace: finish before a later call reuses it.

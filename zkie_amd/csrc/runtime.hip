@@ -195,6 +195,37 @@ int zkie_stream_synchronize(void* stream)
     return ZKIE_OK;
 }
 
+// Streams of the default priority that do not synchronise with the null
+// stream, so that work queued on two of them can overlap.
+int zkie_stream_create(void** stream)
+{
+    if (!stream) return ZKIE_ERR_INVALID;
+    hipStream_t s = nullptr;
+    ZK_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return ZKIE_OK;
+}
+
+int zkie_stream_destroy(void* stream)
+{
+    if (!stream) return ZKIE_ERR_INVALID;
+    ZK_TRY(hipStreamDestroy(as_stream(stream)));
+    return ZKIE_OK;
+}
+
+// Work queued on `waiter` after this call starts once the work queued on
+// `signaler` so far has finished.
+int zkie_stream_wait(void* waiter, void* signaler)
+{
+    hipEvent_t e = nullptr;
+    ZK_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    hipError_t rc = hipEventRecord(e, as_stream(signaler));
+    if (rc == hipSuccess) rc = hipStreamWaitEvent(as_stream(waiter), e, 0);
+    (void)hipEventDestroy(e);  // released once the wait has been satisfied
+    ZK_TRY(rc);
+    return ZKIE_OK;
+}
+
 // Inputs of the synthetic workloads (common/field.rs:17-36 XorShift64,
 // common/fixed_point.rs:11-38 signed embedding v < 0 -> p - |v|).
 int zkie_gen_inputs(uint64_t seed, uint64_t n, int kind, uint64_t* out)
