@@ -66,14 +66,21 @@ def cpu_baseline(wl, rows: int):
     }
 
 
-def leaf_traffic_bytes():
-    """HBM bytes per p2_leaf launch measured with rocprofv3 (FETCH_SIZE +
-    WRITE_SIZE, copy-kernel scaled), from the committed profile summary."""
+# Issue peak of the VALU: 256 CUs x 2.4 GHz x 1.35 wave-instructions per CU
+# per clock, the fastest rate measured on gfx950 (plain 32-bit VOP1/VOP2 ops;
+# v_mad_u64_u32 and other VOP3 forms issue at about 0.86-0.93).
+VALU_PEAK_WINSTR_S = 256 * 2.4e9 * 1.35
+
+
+def leaf_profile():
+    """Per-launch figures of the leaf kernel measured with rocprofv3 at this
+    workload: HBM bytes (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) and VALU
+    wave-instructions, from the committed profile summaries."""
     path = os.path.join(ROOT, "profiles", "p2_leaf_traffic.json")
     if not os.path.exists(path):
-        return None
+        return {}
     with open(path) as f:
-        return json.load(f).get("bytes_per_launch")
+        return json.load(f)
 
 
 def main():
@@ -130,7 +137,8 @@ def main():
     leaf_avg_ms = leaf_ms / max(leaf_n, 1)
     leaf_alg_bytes = n * w * 8 + n * 64       # read the codeword rows, write layer-0 digests
     achieved = leaf_alg_bytes / (leaf_avg_ms * 1e-3) / 1e9 if leaf_avg_ms else 0.0
-    traffic = leaf_traffic_bytes()
+    prof = leaf_profile() if args.config == 3 else {}
+    traffic = prof.get("bytes_per_launch")
     stage_ms = {k: round(ms / max(cnt, 1) * max(cnt, 1) / args.steps, 3) for k, (cnt, ms) in per_kernel.items()}
     # whole-step HBM floor: 8 B in + 32 B codeword + 32 B digests (+ 36 B fold) per input element
     step_alg_bytes = wl.elems * (72 + (36 if wl.fold_k else 0))
@@ -155,6 +163,12 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic, "avg_ms": leaf_avg_ms},
         "step_hbm_frac": step_alg_bytes / t / 1e9 / HBM_PEAK_GBS,
+        # The leaf kernel is bound by VALU issue, not HBM: its rocprof VALU count
+        # over its live duration against the issue peak.
+        "valu_roofline": ({"kernel": "p2_leaf", "achieved": prof["valu_per_launch"] / (leaf_avg_ms * 1e-3),
+                           "peak": VALU_PEAK_WINSTR_S, "unit": "wave-instr/s",
+                           "frac": prof["valu_per_launch"] / (leaf_avg_ms * 1e-3) / VALU_PEAK_WINSTR_S}
+                          if prof.get("valu_per_launch") and leaf_avg_ms else None),
         "stage_ms_per_step": stage_ms,
     }
     if not args.no_cpu_baseline:
