@@ -137,8 +137,9 @@ def test_open_rejects_out_of_range(native, oracle):
         mmcs.open_batches([16], tree)
 
 
-@pytest.mark.parametrize("k,ext", [(1, False), (2, False), (4, False), (6, False), (8, False),
-                                   (1, True), (4, True), (7, True), (0, False)])
+@pytest.mark.parametrize("k,ext", [(1, False), (2, False), (3, False), (4, False), (6, False), (8, False),
+                                   (1, True), (2, True), (3, True), (4, True), (7, True), (0, False),
+                                   (0, True)])
 def test_fold_rows(native, oracle, k, ext):
     _case("fold", k, ext)
     h = 777
