@@ -39,13 +39,14 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(wl, rows: int):
+def cpu_baseline(wl, rows: int, threads: int = 0):
     """The oracle (C restatement of the reference CPU path) on a bounded
-    sample of the same workload, all host cores (OpenMP)."""
+    sample of the same workload, on `threads` host threads (0: all host
+    cores, at most 16, the CPU share of the machine)."""
     from oracle import oracle as O
     from zkie_amd import configs as C
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = threads or min(os.cpu_count() or 1, 16)
     O.set_threads(threads)
     sample = wl.scaled(rows)
     data = O.gen_uniform(C.SEED_DATA, sample.elems).reshape(sample.rows, sample.cols)
@@ -142,6 +143,25 @@ def main():
     stage_ms = {k: round(ms / max(cnt, 1) * max(cnt, 1) / args.steps, 3) for k, (cnt, ms) in per_kernel.items()}
     # whole-step HBM floor: 8 B in + 32 B codeword + 32 B digests (+ 36 B fold) per input element
     step_alg_bytes = wl.elems * (72 + (36 if wl.fold_k else 0))
+    # Per stage: time per step and its algorithmic HBM bytes at the 8 TB/s peak.
+    # LDE: every pass reads and writes the codeword (the first reads the input);
+    # Merkle: rows in, every digest layer written once and read once;
+    # fold: codeword in, one EF element per row out.
+    lg_n = n.bit_length() - 1
+    passes = (lg_n + 8) // 9
+    lde_bytes = wl.elems * 8 + n * w * 8 * (2 * passes - 1)
+    merkle_bytes = n * w * 8 + 2 * (2 * n) * 64
+    fold_bytes = n * w * 8 + n * 16 if wl.fold_k else 0
+
+    def stage(names, alg):
+        ms = sum(per_kernel.get(k, (0, 0.0))[1] for k in names) / args.steps
+        return {"ms": round(ms, 3), "alg_bytes": alg,
+                "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if ms else None}
+
+    stages = {"lde": stage([k for k in per_kernel if k.startswith("ntt_pass")], lde_bytes),
+              "merkle": stage(["p2_leaf", "p2_compress", "p2_subtree"], merkle_bytes)}
+    if wl.fold_k:
+        stages["fold"] = stage(["fold_rows"], fold_bytes)
 
     out = {
         "metric": METRIC,
@@ -170,9 +190,13 @@ def main():
                            "frac": prof["valu_per_launch"] / (leaf_avg_ms * 1e-3) / VALU_PEAK_WINSTR_S}
                           if prof.get("valu_per_launch") and leaf_avg_ms else None),
         "stage_ms_per_step": stage_ms,
+        "stages": stages,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
+        # single-threaded, on a sample 16x smaller (the reference quotes its GPU
+        # speed-up against one CPU thread, whir.rs:55-56)
+        out["cpu_baseline_1thread"] = cpu_baseline(wl, max(args.cpu_rows >> 4, 1 << 10), threads=1)
     print(json.dumps(out), flush=True)
     if args.copy_calibration:
         nbytes = args.copy_calibration << 20
