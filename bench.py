@@ -7,7 +7,7 @@ one fold round (k = 4) over the codeword, on 2^24 rows x 16 columns of
 uniform Goldilocks elements (2^28 input elements). Prints one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N]
-                  [--no-cpu-baseline]
+                  [--no-cpu-baseline] [--prover-data]
 """
 from __future__ import annotations
 
@@ -33,6 +33,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1 << 20,
                     help="coefficient rows of the CPU baseline sample")
+    ap.add_argument("--prover-data", action="store_true",
+                    help="after the timed steps, also time streaming the committed tree out of "
+                         "HBM in the batch-cache prover-data format into a discarding host sink")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the run, copy MIB MiB device to device three times (a plain "
                          "copy kernel of known size for scaling rocprofv3 FETCH/WRITE_SIZE)")
@@ -71,6 +74,25 @@ def cpu_baseline(wl, rows: int, threads: int = 0):
 # per clock, the fastest rate measured on gfx950 (plain 32-bit VOP1/VOP2 ops;
 # v_mad_u64_u32 and other VOP3 forms issue at about 0.86-0.93).
 VALU_PEAK_WINSTR_S = 256 * 2.4e9 * 1.35
+
+
+def prover_data_stream(N, d_cw, n: int, w: int, d_layers, stream, reps: int = 2):
+    """Time zkie_prover_data_write of the step's tree (matrix + digest layers,
+    the bytes after the batch-cache header) into a sink that drops every
+    piece: the device-to-host rate of the stream, without the sink's own cost
+    (a file adds its write rate)."""
+    size = N.prover_data_size(n, w)
+
+    def sink(view):
+        pass
+
+    N.prover_data_write(d_cw.addr, n, w, d_layers.addr, sink, stream.handle)  # first use
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        N.prover_data_write(d_cw.addr, n, w, d_layers.addr, sink, stream.handle)
+    dt = (time.perf_counter() - t0) / reps
+    return {"bytes": size, "ms": round(dt * 1e3, 3), "GB_per_s": round(size / dt / 1e9, 2),
+            "sink": "discard", "path": "HBM -> pinned staging (2 x 16 MiB) -> host callback"}
 
 
 def leaf_profile():
@@ -192,6 +214,8 @@ def main():
         "stage_ms_per_step": stage_ms,
         "stages": stages,
     }
+    if args.prover_data:
+        out["prover_data_stream"] = prover_data_stream(N, d_cw, n, w, d_layers, stream)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
         # single-threaded, on a sample 16x smaller (the reference quotes its GPU

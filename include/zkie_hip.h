@@ -32,6 +32,7 @@ extern "C" {
 #define ZKIE_ERR_INVALID (-1)     /* argument out of range or inconsistent */
 #define ZKIE_ERR_NO_DEVICE (-2)   /* no HIP device */
 #define ZKIE_ERR_ALLOC (-3)       /* device workspace allocation failed */
+#define ZKIE_ERR_IO (-4)          /* a caller's write or read callback failed */
 
 /* ------------------------------------------------------------------------
  * Device and memory. Replace the raw CUDA runtime imports of
@@ -180,6 +181,38 @@ int zkie_mle_eval(const uint64_t *d_vals, uint32_t num_vars, int is_ext, const u
  * (times 2 u64 for EF), row-major. For prefix = 1 the buffers must not overlap. */
 int zkie_whir_encode(const uint64_t *d_poly, uint32_t num_vars, int is_ext, uint32_t log_width,
                      uint32_t log_inv_rate, int prefix, uint64_t *d_out, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Prover-data cache stream. Replaces Whir::serialize_batch_prover_data_into
+ * and Whir::restore_batch_prover_data_from (crates/zkie-core/src/pcs/
+ * whir.rs:542-602, with MerkleTree::write_digest_layers / read_digest_layers
+ * of vendor/p3-merkle-tree/src/merkle_tree.rs:223-276): the bytes of a
+ * committed tree that follow the ZKIEBCH2 header of the batch cache
+ * (pcs/cache.rs:50-57), streamed straight from and to HBM. All integers are
+ * u64 little-endian:
+ *   1 | w | h*w | the h x w matrix | L | L layer lengths | L-1 arities (2) |
+ *   the digest layers (8 u64 per digest, leaves first).
+ * The callbacks receive consecutive pieces of that stream, in order; they
+ * return 0 to continue, anything else stops the call with ZKIE_ERR_IO. A read
+ * callback must fill all `len` bytes. The payload moves through pinned
+ * staging buffers, the copy of the next piece overlapping the callback.
+ * ---------------------------------------------------------------------- */
+typedef int (*zkie_write_fn)(void *ctx, const void *bytes, uint64_t len);
+typedef int (*zkie_read_fn)(void *ctx, void *bytes, uint64_t len);
+/* Total stream length for a tree over an h x w matrix. */
+int zkie_prover_data_size(uint64_t h, uint64_t w, uint64_t *bytes);
+/* whir.rs:542-560: the tree of zkie_merkle_commit (d_mat, d_layers) as bytes. */
+int zkie_prover_data_write(const uint64_t *d_mat, uint64_t h, uint64_t w,
+                           const uint64_t *d_layers, zkie_write_fn write, void *ctx,
+                           void *stream);
+/* whir.rs:572-602: reads a stream written for an h x w matrix back into
+ * d_mat (h*w u64) and d_layers (sum(layer_lens) * 8 u64). Framing that does
+ * not describe a tree of that shape (leaf-matrix count, width, value count,
+ * layer count, layer lengths, arities) returns ZKIE_ERR_INVALID before any of
+ * the part it announces is read. root (host, may be NULL) receives the last
+ * digest layer. */
+int zkie_prover_data_read(zkie_read_fn read, void *ctx, uint64_t h, uint64_t w, uint64_t *d_mat,
+                          uint64_t *d_layers, uint64_t *root, void *stream);
 
 /* ------------------------------------------------------------------------
  * Synthetic inputs (host): XorShift64 of common/field.rs:17-36 seeded with

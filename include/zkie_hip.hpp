@@ -9,7 +9,10 @@
  *   zkie::MerkleTree         <- the MerkleTree prover data (p3-merkle-tree
  *                               merkle_tree.rs:32-70), kept in device memory;
  *   zkie::fold_rows, zkie::mle_eval <- the WHIR row fold and out-of-domain
- *                               evaluation (p3-whir prover/mod.rs:226-290).
+ *                               evaluation (p3-whir prover/mod.rs:226-290);
+ *   zkie::serialize_batch_prover_data_into, zkie::restore_batch_prover_data_from
+ *                            <- the prover-data part of the batch cache
+ *                               (crates/zkie-core/src/pcs/whir.rs:542-602).
  * Matrices are p3's RowMajorMatrix<F> (values row-major, canonical u64).
  * Errors: every non-zero status of the C ABI throws zkie::Error carrying it;
  * there is no CPU fallback here (the reference's Rust caller keeps its own,
@@ -19,6 +22,8 @@
 #include <array>
 #include <cstddef>
 #include <cstdint>
+#include <istream>
+#include <ostream>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -220,6 +225,47 @@ class HipMerkleTreeMmcs {
         return {std::move(opened), PrunedMerklePaths{std::move(pruned)}};
     }
 };
+
+/* Whir::serialize_batch_prover_data_into (whir.rs:542-560): the tree's
+ * matrix and digest layers, framed as the batch cache stores them, streamed
+ * from HBM to `os`. A failing stream throws zkie::Error (ZKIE_ERR_IO). */
+inline void serialize_batch_prover_data_into(const MerkleTree& t, std::ostream& os)
+{
+    zkie_write_fn write = [](void* ctx, const void* bytes, uint64_t len) -> int {
+        auto* s = static_cast<std::ostream*>(ctx);
+        s->write(static_cast<const char*>(bytes), static_cast<std::streamsize>(len));
+        return s->good() ? 0 : 1;
+    };
+    check(zkie_prover_data_write(t.mat.data(), t.height, t.width, t.layers.data(), write, &os, nullptr),
+          "zkie_prover_data_write");
+}
+
+/* Whir::restore_batch_prover_data_from (whir.rs:572-602): a tree over an
+ * h x w matrix (the table shape the caller knows) read from `is` into new
+ * device buffers. Framing of another shape throws zkie::Error. */
+inline MerkleTree restore_batch_prover_data_from(std::istream& is, size_t h, size_t w)
+{
+    MerkleTree t;
+    t.height = h;
+    t.width = w;
+    uint32_t nl = 0;
+    std::vector<uint64_t> lens(65);
+    check(zkie_merkle_layout(h, &nl, lens.data()), "zkie_merkle_layout");
+    lens.resize(nl);
+    size_t total = 0;
+    for (uint64_t l : lens) total += l;
+    t.layer_lens = lens;
+    t.mat = DeviceBuffer(h * w);
+    t.layers = DeviceBuffer(total * 8);
+    zkie_read_fn read = [](void* ctx, void* bytes, uint64_t len) -> int {
+        auto* s = static_cast<std::istream*>(ctx);
+        s->read(static_cast<char*>(bytes), static_cast<std::streamsize>(len));
+        return s->gcount() == static_cast<std::streamsize>(len) ? 0 : 1;
+    };
+    check(zkie_prover_data_read(read, &is, h, w, t.mat.data(), t.layers.data(), t.root.data(), nullptr),
+          "zkie_prover_data_read");
+    return t;
+}
 
 /* Row fold (prover/mod.rs:257-290; mle.rs:8-22 with variable 0 the least
  * significant bit) of every row of a device matrix of 2^k (EF: 2^(k+1)) u64 per row. */

@@ -364,6 +364,53 @@ def whir_encode(poly, num_vars: int, is_ext: bool, log_width: int, log_inv_rate:
     return lde_batch(np.ascontiguousarray(m).reshape(rows, cols * E), log_inv_rate)
 
 
+# ---- prover-data cache stream -------------------------------------------------
+def prover_data_bytes(mat, layers) -> bytes:
+    """Whir::serialize_batch_prover_data_into (crates/zkie-core/src/pcs/whir.rs:542-560)
+    of a tree over one matrix, then MerkleTree::write_digest_layers
+    (vendor/p3-merkle-tree/src/merkle_tree.rs:223-243). Little-endian u64s:
+    leaf-matrix count, width, value count, the values; layer count, layer
+    lengths, arities (2 for the binary tree: merkle_tree.rs:146-158 with N = 2),
+    the digests."""
+    m = u64(mat)
+    h, w = m.shape
+    lay = [np.asarray(l, np.uint64).reshape(-1, 8) for l in layers]
+    frame = [len(lay)] + [l.shape[0] for l in lay] + [2] * (len(lay) - 1)
+    parts = [np.array([1, w, h * w], "<u8").tobytes(), m.astype("<u8").tobytes(),
+             np.array(frame, "<u8").tobytes()]
+    parts += [l.astype("<u8").tobytes() for l in lay]
+    return b"".join(parts)
+
+
+def parse_prover_data(buf: bytes):
+    """Whir::restore_batch_prover_data_from (whir.rs:572-602) and
+    MerkleTree::read_digest_layers (merkle_tree.rs:247-276): returns
+    (matrices as (h, w) arrays, digest layers as (len, 8) arrays, arities).
+    Raises ValueError on a stream that ends early or has bytes left over."""
+    pos = 0
+
+    def take(n_u64: int) -> np.ndarray:
+        nonlocal pos
+        end = pos + 8 * n_u64
+        if end > len(buf):
+            raise ValueError("prover-data stream ends early")
+        a = np.frombuffer(buf, "<u8", n_u64, pos).astype(np.uint64)
+        pos = end
+        return a
+
+    mats = []
+    for _ in range(int(take(1)[0])):
+        w, n = (int(x) for x in take(2))
+        mats.append(take(n).reshape(-1, w) if w else take(n))
+    nl = int(take(1)[0])
+    lens = [int(x) for x in take(nl)]
+    arities = [int(x) for x in take(max(nl - 1, 0))]
+    layers = [take(8 * ln).reshape(ln, 8) for ln in lens]
+    if pos != len(buf):
+        raise ValueError("bytes left after the digest layers")
+    return mats, layers, arities
+
+
 # ---- inputs ------------------------------------------------------------------
 def xorshift(seed: int, n: int):
     st = np.zeros(1, np.uint64)

@@ -1,10 +1,13 @@
 // Parity test of the C++ host interface (include/zkie_hip.hpp) against the
 // oracle, written like the reference's own engine tests: transform and
 // inverse round trip, encode, commit, open, verify, pruned multi-opening,
-// fold, and the error path. Needs a HIP device; prints one line per check and
+// fold, the prover-data cache stream, and the error paths. Needs a HIP device; prints one line per check and
 // exits non-zero on the first mismatch.
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
+#include <sstream>
+#include <string>
 #include <vector>
 
 #include "zkie_hip.hpp"
@@ -106,9 +109,47 @@ int main()
     same = true;
     for (size_t i = 0; i < h; i++) same = same && f[i][0] == fref[2 * i] && f[i][1] == fref[2 * i + 1];
     EXPECT(same, "fold_rows equals the oracle");
+    bool threw = false;
+
+    // prover-data cache stream (whir.rs:542-602): framing, payload, round trip
+    std::stringstream ss(std::ios::in | std::ios::out | std::ios::binary);
+    zkie::serialize_batch_prover_data_into(tree, ss);
+    const std::string bytes = ss.str();
+    uint64_t size = 0;
+    zkie::check(zkie_prover_data_size(h, 16, &size), "zkie_prover_data_size");
+    auto u64_at = [&](size_t i) {
+        uint64_t v = 0;
+        std::memcpy(&v, bytes.data() + 8 * i, 8);
+        return v;
+    };
+    const size_t L = tree.layer_lens.size(), t0 = 3 + h * 16, d0 = t0 + 2 * L;
+    size_t total = 0;
+    for (uint64_t l : tree.layer_lens) total += l;
+    same = bytes.size() == size && size == 8 * (d0 + 8 * total);
+    same = same && u64_at(0) == 1 && u64_at(1) == 16 && u64_at(2) == h * 16 && u64_at(t0) == L;
+    for (size_t i = 0; same && i < h * 16; i++) same = u64_at(3 + i) == cw.values[i];
+    for (size_t i = 0; same && i < L; i++) same = u64_at(t0 + 1 + i) == tree.layer_lens[i];
+    for (size_t i = 0; same && i + 1 < L; i++) same = u64_at(t0 + 1 + L + i) == 2;
+    for (size_t i = 0; same && i < 8 * total; i++) same = u64_at(d0 + i) == layers_ref[i];
+    EXPECT(same, "serialize_batch_prover_data_into frames the codeword and the oracle's layers");
+    ss.seekg(0);
+    const auto back = zkie::restore_batch_prover_data_from(ss, h, 16);
+    EXPECT(back.root == cap[0] && back.mat.download() == cw.values && back.layers.download() == tree.layers.download(),
+           "restore_batch_prover_data_from returns the committed tree");
+    const auto o1 = mmcs.open_batch(777, tree), o2 = mmcs.open_batch(777, back);
+    EXPECT(o1.opened_values == o2.opened_values && o1.opening_proof == o2.opening_proof,
+           "the restored tree opens like the committed one");
+    std::stringstream other(bytes);
+    threw = false;
+    try {
+        (void)zkie::restore_batch_prover_data_from(other, h, 8);
+    } catch (const zkie::Error& e) {
+        threw = e.code == ZKIE_ERR_INVALID;
+    }
+    EXPECT(threw, "restoring a stream of another shape throws zkie::Error(ZKIE_ERR_INVALID)");
 
     // error path: an index outside the tree is a status, thrown as zkie::Error
-    bool threw = false;
+    threw = false;
     try {
         (void)mmcs.open_batch(h, tree);
     } catch (const zkie::Error& e) {

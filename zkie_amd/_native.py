@@ -50,6 +50,9 @@ SIGNATURES = {
     "zkie_fold_rows_at": [_vp, _u64, _u32, _int, _u64p, _u64, _u64p, _u64p, _vp],
     "zkie_mle_eval": [_vp, _u32, _int, _u64p, _u64p, _vp],
     "zkie_whir_encode": [_vp, _u32, _int, _u32, _u32, _int, _vp, _vp],
+    "zkie_prover_data_size": [_u64, _u64, _u64p],
+    "zkie_prover_data_write": [_vp, _u64, _u64, _vp, _vp, _vp, _vp],
+    "zkie_prover_data_read": [_vp, _vp, _u64, _u64, _vp, _vp, _u64p, _vp],
     "zkie_gen_inputs": [_u64, _u64, _int, _u64p],
     "zkie_profile_enable": [_int],
     "zkie_profile_reset": [],
@@ -152,6 +155,63 @@ def merkle_layout(h: int):
     lens = np.zeros(65, np.uint64)
     check(load().zkie_merkle_layout(h, ctypes.byref(nl), p(lens)), "zkie_merkle_layout")
     return [int(x) for x in lens[: nl.value]]
+
+
+# zkie_write_fn / zkie_read_fn: int (*)(void* ctx, void* bytes, uint64_t len)
+IO_FN = ctypes.CFUNCTYPE(_int, _vp, _vp, _u64)
+
+
+def prover_data_size(h: int, w: int) -> int:
+    n = ctypes.c_uint64()
+    check(load().zkie_prover_data_size(h, w, ctypes.byref(n)), "zkie_prover_data_size")
+    return int(n.value)
+
+
+def _view(ptr: int, n: int) -> memoryview:
+    return memoryview((ctypes.c_char * n).from_address(ptr)).cast("B")
+
+
+def prover_data_write(d_mat: int, h: int, w: int, d_layers: int, sink, stream=None) -> None:
+    """Stream the prover data to sink(view) piece by piece; each view is only
+    valid during its call. An exception raised by sink propagates."""
+    err = []
+
+    def cb(_ctx, ptr, n):
+        try:
+            sink(_view(ptr, n))
+            return 0
+        except BaseException as e:  # noqa: BLE001 - re-raised below
+            err.append(e)
+            return 1
+
+    fn = IO_FN(cb)
+    rc = load().zkie_prover_data_write(d_mat, h, w, d_layers, ctypes.cast(fn, _vp), None, stream)
+    if err:
+        raise err[0]
+    check(rc, "zkie_prover_data_write")
+
+
+def prover_data_read(source, h: int, w: int, d_mat: int, d_layers: int, stream=None) -> np.ndarray:
+    """Fill the device matrix and layers from source(view), which must fill the
+    whole view (a short fill or an exception stops the call). Returns the root."""
+    err = []
+
+    def cb(_ctx, ptr, n):
+        try:
+            source(_view(ptr, n))
+            return 0
+        except BaseException as e:  # noqa: BLE001 - re-raised below
+            err.append(e)
+            return 1
+
+    fn = IO_FN(cb)
+    root = np.zeros(8, np.uint64)
+    rc = load().zkie_prover_data_read(ctypes.cast(fn, _vp), None, h, w, d_mat, d_layers, p(root),
+                                      stream)
+    if err:
+        raise err[0]
+    check(rc, "zkie_prover_data_read")
+    return root
 
 
 GEN_UNIFORM, GEN_I16, GEN_I8, GEN_GAUSS_I16 = 0, 1, 2, 3

@@ -10,7 +10,10 @@ Mirrors the engines of the reference's WHIR wrapper:
   * fold_rows         <- the WHIR row fold (p3-whir prover/mod.rs:257-290);
     fold_rows_at      <- its queried-row form (prover/mod.rs:265-290);
   * mle_eval          <- the OOD answer sumcheck_prover.eval (prover/mod.rs:226-236);
-  * whir_encode       <- commit_extension's encoding (committer/writer.rs:21-86).
+  * whir_encode       <- commit_extension's encoding (committer/writer.rs:21-86);
+  * serialize_batch_prover_data_into / restore_batch_prover_data_from
+                      <- the prover-data part of the batch cache
+                         (crates/zkie-core/src/pcs/whir.rs:542-602).
 Unlike the reference there is no CPU fallback: every failure raises.
 """
 from __future__ import annotations
@@ -145,6 +148,40 @@ class HipMerkleTreeMmcs:
             tree.d_mat.addr, tree.h, tree.w, tree.d_layers.addr, N.p(idx), n, N.p(rows),
             N.p(out), cap, ctypes.byref(count), None), "zkie_merkle_open_pruned")
         return rows, out[: count.value]
+
+
+def serialize_batch_prover_data_into(tree: HipMerkleTree, writer, stream=None) -> int:
+    """Whir::serialize_batch_prover_data_into (crates/zkie-core/src/pcs/whir.rs:542-560):
+    write the committed matrix and its digest layers to the binary stream
+    `writer` (anything with .write), straight from HBM. Returns the byte count."""
+    n = [0]
+
+    def sink(view):
+        writer.write(view)
+        n[0] += len(view)
+
+    N.prover_data_write(tree.d_mat.addr, tree.h, tree.w, tree.d_layers.addr, sink, stream)
+    return n[0]
+
+
+def restore_batch_prover_data_from(reader, h: int, w: int, stream=None) -> HipMerkleTree:
+    """Whir::restore_batch_prover_data_from (whir.rs:572-602): read a stream
+    written for an h x w matrix (the table shape the caller already knows) into
+    new device buffers. Framing of another shape raises ZkieError; a stream
+    that ends early raises EOFError."""
+
+    def source(view):
+        got = 0
+        while got < len(view):
+            k = reader.readinto(view[got:])
+            if not k:
+                raise EOFError("prover-data stream ended early")
+            got += k
+
+    d_mat = DeviceBuffer(h * w)
+    d_layers = DeviceBuffer(sum(N.merkle_layout(h)) * 8)
+    root = N.prover_data_read(source, h, w, d_mat.addr, d_layers.addr, stream)
+    return HipMerkleTree(d_mat, h, w, d_layers, root)
 
 
 def fold_rows_device(d_mat: DeviceBuffer, h: int, k: int, r, is_ext: bool, d_out: DeviceBuffer,
