@@ -23,14 +23,28 @@ void run_pass_t(const PassArgs& a, uint32_t T)
     const uint64_t blocks = pass_blocks(a);
     std::vector<uint64_t> lds(pass_lds_bytes(a) / 8 + 1);
     constexpr int n = pass_steps<S>();
-    if (T % (1u << (a.logC + a.logJ)) != 0) std::abort();  // a thread keeps one vector lane
+    const uint32_t logV = a.logC + a.logJ;
+    if (T % (1u << logV) != 0) std::abort();  // a thread keeps one vector lane
+    // the kernel's order: step-0 reads, LDS tables, [barrier] the rest of
+    // step 0, then [barrier] each later step (one round of step-0 items when
+    // T is the kernel's thread count; more rounds go through pass_step)
+    const bool split0 = n > 1 && ((1u << (S - Radix<S>::r0)) << logV) <= kStepU * T;
+    using Regs = uint64_t[kStepU][1 << Radix<S>::r0];
+    std::vector<Regs> x(T);
     for (uint64_t bid = 0; bid < blocks; bid++) {
         const PassTile t = pass_tile(a, bid);
-        for (uint32_t tid = 0; tid < T; tid++) pass_prologue<S, ROLE>(a, t, tid, T, lds.data());
-        for (int k = 0; k < n; k++)  // a barrier separates consecutive steps
+        if (split0)
+            for (uint32_t tid = 0; tid < T; tid++)
+                pass_step0_gather<S, KNZ, LOGV>(a, t, pass_lane(a, t, tid), tid, T, x[tid]);
+        for (uint32_t tid = 0; tid < T; tid++) pass_tables<S, ROLE>(a, t, tid, T, lds.data());
+        for (int k = 0; k < n; k++)
             for (uint32_t tid = 0; tid < T; tid++) {
                 const PassLane l = pass_lane(a, t, tid);
-                pass_step<S, KNZ, INV, ROLE, LOGV>(k, a, t, l, tid, T, lds.data());
+                if (k == 0 && split0) {
+                    if constexpr (n > 1) pass_step0_finish<S, INV, ROLE, LOGV>(a, t, l, tid, T, lds.data(), x[tid]);
+                } else {
+                    pass_step<S, KNZ, INV, ROLE, LOGV>(k, a, t, l, tid, T, lds.data());
+                }
             }
     }
 }

@@ -65,10 +65,29 @@ def test_dft_passes(emu, oracle, lg, w):
     assert (y == x).all()
 
 
+# 512 threads per workgroup, the kernel's own count (one round per step).
+@pytest.mark.parametrize("lg,w", [(13, 16), (18, 16), (10, 16), (12, 32), (9, 16), (14, 8), (19, 16)])
+def test_dft_passes_kernel_threads(emu, oracle, lg, w):
+    x = oracle.gen_uniform(lg * 10 + w, (1 << lg) * w).reshape(1 << lg, w)
+    y = x.copy()
+    assert emu.emu_dft(ptr(y), lg, w, 0, 512) == 0
+    assert (y == oracle.dft_batch(x)).all()
+    assert emu.emu_dft(ptr(y), lg, w, 1, 512) == 0
+    assert (y == x).all()
+
+
 @pytest.mark.parametrize("lg,w,lb", [(4, 1, 2), (10, 16, 2), (16, 1, 2), (9, 32, 3), (12, 16, 1),
                                      (16, 16, 2), (14, 16, 3), (11, 128, 1), (7, 1, 2), (2, 3, 4)])
 def test_lde_passes(emu, oracle, lg, w, lb):
     x = oracle.gen_uniform(7, (1 << lg) * w).reshape(1 << lg, w)
     out = np.zeros(((1 << lg) << lb, w), np.uint64)
     assert emu.emu_lde(ptr(x), 1 << lg, w, lb, ptr(out), 256) == 0
+    assert (out == oracle.lde_batch(x, lb)).all()
+
+
+@pytest.mark.parametrize("lg,w,lb", [(16, 16, 2), (14, 16, 3), (17, 16, 2)])
+def test_lde_passes_kernel_threads(emu, oracle, lg, w, lb):
+    x = oracle.gen_uniform(8, (1 << lg) * w).reshape(1 << lg, w)
+    out = np.zeros(((1 << lg) << lb, w), np.uint64)
+    assert emu.emu_lde(ptr(x), 1 << lg, w, lb, ptr(out), 512) == 0
     assert (out == oracle.lde_batch(x, lb)).all()

@@ -49,26 +49,39 @@ template <int S, int KNZ, bool INV, int ROLE, int LOGV>
 __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 {
     extern __shared__ uint64_t lds[];
+    // The launch always uses kNttThreads threads; a compile-time count lets
+    // the step loops unroll to their exact number of rounds.
+    constexpr uint32_t T = kNttThreads;
+    const uint32_t tid = threadIdx.x;
+    constexpr int n = pass_steps<S>();
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
     const PassTile t = pass_tile(a, bid);
-    const PassLane l = pass_lane(a, t, threadIdx.x);
-    constexpr int n = pass_steps<S>();
-    pass_prologue<S, ROLE>(a, t, threadIdx.x, blockDim.x, lds);
-    pass_step<S, KNZ, INV, ROLE, LOGV>(0, a, t, l, threadIdx.x, blockDim.x, lds);
-    if (n > 1) {
+    const PassLane l = pass_lane(a, t, tid);
+    if constexpr (n == 1) {
+        pass_step<S, KNZ, INV, ROLE, LOGV>(0, a, t, l, tid, T, lds);
+    } else {
+        static_assert(((1u << (S - Radix<S>::r0)) << 4) <= kStepU * T, "step 0 in one round");
+        // The tile's HBM reads go out first; the twiddle tables are filled in
+        // LDS while they are in flight, so the two latencies overlap.
+        uint64_t x[kStepU][1 << Radix<S>::r0];
+        pass_step0_gather<S, KNZ, LOGV>(a, t, l, tid, T, x);
+        pass_tables<S, ROLE>(a, t, tid, T, lds);
+        __syncthreads();  // step twiddles in LDS before step 0 reads them
+        pass_step0_finish<S, INV, ROLE, LOGV>(a, t, l, tid, T, lds, x);
         __syncthreads();
-        pass_step<S, KNZ, INV, ROLE, LOGV>(1, a, t, l, threadIdx.x, blockDim.x, lds);
+        pass_step<S, KNZ, INV, ROLE, LOGV>(1, a, t, l, tid, T, lds);
     }
     if (n > 2) {
         __syncthreads();
-        pass_step<S, KNZ, INV, ROLE, LOGV>(2, a, t, l, threadIdx.x, blockDim.x, lds);
+        pass_step<S, KNZ, INV, ROLE, LOGV>(2, a, t, l, tid, T, lds);
     }
 }
 
-// Launch one instantiation; dynamic LDS above the 64 KB default needs the
-// kernel's limit raised first (gfx950 has 160 KB of LDS per CU).
+// Launch one instantiation, one workgroup per tile; dynamic LDS above the
+// 64 KB default needs the kernel's limit raised first (gfx950 has 160 KB of
+// LDS per CU).
 template <int S, int KNZ, bool INV, int ROLE, int LOGV>
-hipError_t launch_one(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_one(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
 {
     static size_t raised = 64 * 1024;
     if (shmem > raised) {
@@ -77,63 +90,71 @@ hipError_t launch_one(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
         if (e != hipSuccess) return e;
         raised = shmem;
     }
+    dim3 grid;
+    if (blocks <= 0x7FFFFFFFull) {
+        grid = dim3((unsigned)blocks, 1, 1);
+    } else {
+        const uint64_t gx = 65536;
+        if ((blocks % gx) != 0) return hipErrorInvalidValue;
+        grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
+    }
     ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV><<<grid, kNttThreads, shmem, s>>>(a);
     return hipGetLastError();
 }
 
 // Tiles of 16 vector lanes (the usual case) address LDS with immediate offsets.
 template <int S, int KNZ, bool INV, int ROLE>
-hipError_t launch_v(const PassArgs& a, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_v(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
 {
-    if (a.logC + a.logJ == 4) return launch_one<S, KNZ, INV, ROLE, 4>(a, grid, shmem, s);
-    return launch_one<S, KNZ, INV, ROLE, -1>(a, grid, shmem, s);
+    if (a.logC + a.logJ == 4) return launch_one<S, KNZ, INV, ROLE, 4>(a, blocks, shmem, s);
+    return launch_one<S, KNZ, INV, ROLE, -1>(a, blocks, shmem, s);
 }
 
 // Instances: forward passes prune zero inputs of an LDE (KNZ < 8) and never
 // scale; inverse passes read full inputs and scale in the last pass.
 template <int S, bool INV, int ROLE>
-hipError_t launch_pass_r(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_pass_r(const PassArgs& a, int knz, uint64_t blocks, size_t shmem, hipStream_t s)
 {
-    if (INV) return launch_v<S, 8, INV, ROLE>(a, grid, shmem, s);
+    if (INV) return launch_v<S, 8, INV, ROLE>(a, blocks, shmem, s);
     switch (knz) {
-        case 1: return launch_v<S, 1, INV, ROLE>(a, grid, shmem, s);
-        case 2: return launch_v<S, 2, INV, ROLE>(a, grid, shmem, s);
-        case 4: return launch_v<S, 4, INV, ROLE>(a, grid, shmem, s);
-        default: return launch_v<S, 8, INV, ROLE>(a, grid, shmem, s);
+        case 1: return launch_v<S, 1, INV, ROLE>(a, blocks, shmem, s);
+        case 2: return launch_v<S, 2, INV, ROLE>(a, blocks, shmem, s);
+        case 4: return launch_v<S, 4, INV, ROLE>(a, blocks, shmem, s);
+        default: return launch_v<S, 8, INV, ROLE>(a, blocks, shmem, s);
     }
 }
 
 template <int S, bool INV>
-hipError_t launch_pass_s(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_pass_s(const PassArgs& a, int knz, uint64_t blocks, size_t shmem, hipStream_t s)
 {
     switch (pass_role(a)) {
-        case kRoleTwiddle: return launch_pass_r<S, INV, kRoleTwiddle>(a, knz, grid, shmem, s);
-        case kRoleTable: return launch_pass_r<S, INV, kRoleTable>(a, knz, grid, shmem, s);
+        case kRoleTwiddle: return launch_pass_r<S, INV, kRoleTwiddle>(a, knz, blocks, shmem, s);
+        case kRoleTable: return launch_pass_r<S, INV, kRoleTable>(a, knz, blocks, shmem, s);
         default:
             // A forward last pass never scales and an inverse one always does (1/n, n > 1).
             if constexpr (INV) {
                 if (pass_role(a) != kRoleLastScale) return hipErrorInvalidValue;
-                return launch_pass_r<S, INV, kRoleLastScale>(a, knz, grid, shmem, s);
+                return launch_pass_r<S, INV, kRoleLastScale>(a, knz, blocks, shmem, s);
             } else {
                 if (pass_role(a) != kRoleLast) return hipErrorInvalidValue;
-                return launch_pass_r<S, INV, kRoleLast>(a, knz, grid, shmem, s);
+                return launch_pass_r<S, INV, kRoleLast>(a, knz, blocks, shmem, s);
             }
     }
 }
 
 template <bool INV>
-hipError_t launch_pass(const PassArgs& a, int knz, dim3 grid, size_t shmem, hipStream_t s)
+hipError_t launch_pass(const PassArgs& a, int knz, uint64_t blocks, size_t shmem, hipStream_t s)
 {
     switch (a.s) {
-        case 1: return launch_pass_s<1, INV>(a, knz, grid, shmem, s);
-        case 2: return launch_pass_s<2, INV>(a, knz, grid, shmem, s);
-        case 3: return launch_pass_s<3, INV>(a, knz, grid, shmem, s);
-        case 4: return launch_pass_s<4, INV>(a, knz, grid, shmem, s);
-        case 5: return launch_pass_s<5, INV>(a, knz, grid, shmem, s);
-        case 6: return launch_pass_s<6, INV>(a, knz, grid, shmem, s);
-        case 7: return launch_pass_s<7, INV>(a, knz, grid, shmem, s);
-        case 8: return launch_pass_s<8, INV>(a, knz, grid, shmem, s);
-        default: return launch_pass_s<9, INV>(a, knz, grid, shmem, s);
+        case 1: return launch_pass_s<1, INV>(a, knz, blocks, shmem, s);
+        case 2: return launch_pass_s<2, INV>(a, knz, blocks, shmem, s);
+        case 3: return launch_pass_s<3, INV>(a, knz, blocks, shmem, s);
+        case 4: return launch_pass_s<4, INV>(a, knz, blocks, shmem, s);
+        case 5: return launch_pass_s<5, INV>(a, knz, blocks, shmem, s);
+        case 6: return launch_pass_s<6, INV>(a, knz, blocks, shmem, s);
+        case 7: return launch_pass_s<7, INV>(a, knz, blocks, shmem, s);
+        case 8: return launch_pass_s<8, INV>(a, knz, blocks, shmem, s);
+        default: return launch_pass_s<9, INV>(a, knz, blocks, shmem, s);
     }
 }
 
@@ -161,17 +182,9 @@ int run_passes(const Plan& p, uint64_t w, const uint64_t* in, uint64_t in_rows, 
     for (uint32_t i = 0; i < p.np; i++) {
         const PassArgs a = pass_args(p, i, B, w, in, in_rows, tmp, out, tables, inverse);
         const uint64_t blocks = pass_blocks(a);
-        dim3 grid;
-        if (blocks <= 0x7FFFFFFFull) {
-            grid = dim3((unsigned)blocks, 1, 1);
-        } else {
-            const uint64_t gx = 65536;
-            if ((blocks % gx) != 0) return ZKIE_ERR_INVALID;
-            grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
-        }
         ProfMark m = prof_begin(a.last ? "ntt_pass_last" : (i == 0 ? "ntt_pass_first" : "ntt_pass_mid"), s);
-        const hipError_t e = inverse ? launch_pass<true>(a, pass_knz(a), grid, pass_lds_bytes(a), s)
-                                     : launch_pass<false>(a, pass_knz(a), grid, pass_lds_bytes(a), s);
+        const hipError_t e = inverse ? launch_pass<true>(a, pass_knz(a), blocks, pass_lds_bytes(a), s)
+                                     : launch_pass<false>(a, pass_knz(a), blocks, pass_lds_bytes(a), s);
         prof_end(m, s);
         ZK_TRY(e);
         B -= a.s;

@@ -265,108 +265,151 @@ __host__ __device__ __forceinline__ PassLane pass_lane(const PassArgs& a, const 
     return l;
 }
 
-// One radix-2^RL DIF step on sub-problems of 2^BS points of an S-point DFT.
-// FROM_GLOBAL: inputs from HBM (step 0; only the first KNZ of the R inputs
-// can be non-zero, the rest are the zero padding of an LDE). TO_GLOBAL:
-// outputs to HBM (last step). LOGV is the tile's log2 vector width when known
-// at compile time (then LDS addresses are a base plus immediate offsets), or
-// -1 to read it from the tile.
-template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE, int LOGV>
-__host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, const PassLane& l,
-                                                  uint32_t tid, uint32_t T, uint64_t* lds, const uint64_t* twtab)
+// Items of a step (one per sub-problem q and vector lane): item `it` works
+// on the points base + k 2^(BS - RL) of its block.
+template <int RL, int BS>
+__host__ __device__ __forceinline__ void step_item(uint32_t it, uint32_t logV, uint32_t& base, uint32_t& q)
+{
+    constexpr int QL = BS - RL;
+    const uint32_t rest = it >> logV;
+    q = rest & ((1u << QL) - 1);
+    base = ((rest >> QL) << BS) + q;
+}
+
+// A thread takes U items per round and issues all their reads before any
+// arithmetic, so that U * R reads are in flight per thread.
+constexpr int kStepU = 2;
+
+// Reads of one round of a radix-2^RL DIF step on sub-problems of 2^BS points
+// of an S-point DFT: the R points of items it0 and it0 + T into x.
+// FROM_GLOBAL: from HBM (step 0; only the first KNZ of the R inputs can be
+// non-zero, the rest are the zero padding of an LDE), else from the LDS tile.
+// LOGV is the tile's log2 vector width when known at compile time (then LDS
+// addresses are a base plus immediate offsets), or -1 to read it from the tile.
+template <int S, int RL, int BS, int KNZ, bool FROM_GLOBAL, int LOGV>
+__host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const PassTile& t, const PassLane& l,
+                                                     uint32_t it0, uint32_t T, const uint64_t* lds,
+                                                     uint64_t (&x)[kStepU][1 << RL])
 {
     constexpr int R = 1 << RL;
     constexpr int QL = BS - RL;
-    // A thread takes U items per round and issues all their reads before any
-    // arithmetic, so that U * R reads are in flight per thread.
-    constexpr int U = 2;
     const uint32_t logV = LOGV >= 0 ? (uint32_t)LOGV : t.logV;
     const uint32_t items = (1u << (S - RL)) << logV;
     const uint32_t v = l.v;
-    for (uint32_t it0 = tid; it0 < items; it0 += U * T) {
-        uint64_t x[U][R];
-        uint64_t tw[U][R];  // step twiddles w_{2^BS}^(f q), read with the data
-        uint32_t base[U], q[U];
-        bool live[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t it = it0 + (uint32_t)u * T;
-            live[u] = it < items;
-            const uint32_t rest = it >> logV;
-            q[u] = rest & ((1u << QL) - 1);
-            base[u] = ((rest >> QL) << BS) + q[u];
-            if (!live[u]) continue;
-            const uint64_t gbase = l.in_base + (uint64_t)base[u] * a.in_stride;
-            const uint32_t lbase = (base[u] << logV) | v;
+    for (int u = 0; u < kStepU; u++) {
+        const uint32_t it = it0 + (uint32_t)u * T;
+        if (it >= items) continue;
+        uint32_t base, q;
+        step_item<RL, BS>(it, logV, base, q);
+        const uint64_t gbase = l.in_base + (uint64_t)base * a.in_stride;
+        const uint32_t lbase = (base << logV) | v;
 #pragma unroll
-            for (int k = 0; k < R; k++) {
-                const uint32_t pos = base[u] + ((uint32_t)k << QL);
-                if (FROM_GLOBAL) {
-                    if (k < KNZ && (!a.check_rows || pos < l.pos_lim)) {
-                        const uint64_t idx = gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride;
-                        ZK_BOUND(idx, a.in_len);
-                        x[u][k] = a.in[idx];
-                    } else {
-                        x[u][k] = 0;
-                    }
+        for (int k = 0; k < R; k++) {
+            const uint32_t pos = base + ((uint32_t)k << QL);
+            if (FROM_GLOBAL) {
+                if (k < KNZ && (!a.check_rows || pos < l.pos_lim)) {
+                    const uint64_t idx = gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride;
+                    ZK_BOUND(idx, a.in_len);
+                    x[u][k] = a.in[idx];
                 } else {
-                    const uint32_t li = lbase + (((uint32_t)k << QL) << logV);
-                    ZK_BOUND(li, (1u << S) << logV);
-                    x[u][k] = lds[li];
-                }
-            }
-            if (QL > 0) {
-#pragma unroll
-                for (int idx = 1; idx < R; idx++) {
-                    const uint32_t f = bit_reverse((uint32_t)idx, RL);
-                    tw[u][idx] = a.w512[(f * q[u]) << (kStepTableLg - BS)];
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (!live[u]) continue;
-            dft_small<RL, INV>(x[u]);
-            if (QL > 0) {
-#pragma unroll
-                for (int idx = 1; idx < R; idx++) x[u][idx] = gl_mul(x[u][idx], tw[u][idx]);
-            }
-            if (TO_GLOBAL) {
-                // QL == 0 here: base holds the leading digits, f the last one,
-                // which digit reversal moves to the top of i1.
-                const uint32_t i1b = digit_reverse<S>(base[u]);
-                const uint64_t obase = l.out_base + (uint64_t)i1b * a.out_stride;
-#pragma unroll
-                for (int idx = 0; idx < R; idx++) {
-                    const uint32_t f = bit_reverse((uint32_t)idx, RL);
-                    const uint32_t fi = f << (S - RL);
-                    const uint32_t i1 = i1b + fi;
-                    uint64_t val = x[u][idx];
-                    if (ROLE == kRoleTable) {
-                        ZK_BOUND(i1, 1u << a.s);
-                        val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
-                    } else if (ROLE == kRoleTwiddle) {
-                        const uint64_t ex = (uint64_t)i1 * l.j2;
-                        if (ex) val = gl_mul(val, pass_root_pow(a, ex));
-                    } else {
-                        if (ROLE == kRoleLastScale) val = gl_mul(val, a.scale);
-                        val = gl_canon(val);
-                    }
-                    const uint64_t oidx = obase + (uint64_t)fi * a.out_stride;
-                    ZK_BOUND(oidx, a.out_len);
-                    a.out[oidx] = val;
+                    x[u][k] = 0;
                 }
             } else {
-                const uint32_t lbase = (base[u] << logV) | v;
-#pragma unroll
-                for (int idx = 0; idx < R; idx++) {
-                    const uint32_t f = bit_reverse((uint32_t)idx, RL);
-                    const uint32_t li = lbase + ((f << QL) << logV);
-                    ZK_BOUND(li, (1u << S) << logV);
-                    lds[li] = x[u][idx];
-                }
+                const uint32_t li = lbase + (((uint32_t)k << QL) << logV);
+                ZK_BOUND(li, (1u << S) << logV);
+                x[u][k] = lds[li];
             }
         }
+    }
+}
+
+// The rest of the round: R-point DFT of each item, step twiddles
+// w_{2^BS}^(f q) from the LDS table wtab (w_512^k), then the outputs to the
+// LDS tile or, in the last step (TO_GLOBAL), with the pass role's treatment
+// to HBM.
+template <int S, int RL, int BS, bool INV, bool TO_GLOBAL, int ROLE, int LOGV>
+__host__ __device__ __forceinline__ void step_finish(const PassArgs& a, const PassTile& t, const PassLane& l,
+                                                     uint32_t it0, uint32_t T, uint64_t* lds,
+                                                     const uint64_t* wtab, const uint64_t* twtab,
+                                                     uint64_t (&x)[kStepU][1 << RL])
+{
+    constexpr int R = 1 << RL;
+    constexpr int QL = BS - RL;
+    const uint32_t logV = LOGV >= 0 ? (uint32_t)LOGV : t.logV;
+    const uint32_t items = (1u << (S - RL)) << logV;
+    const uint32_t v = l.v;
+#pragma unroll
+    for (int u = 0; u < kStepU; u++) {
+        const uint32_t it = it0 + (uint32_t)u * T;
+        if (it >= items) continue;
+        uint32_t base, q;
+        step_item<RL, BS>(it, logV, base, q);
+        uint64_t tw[R];
+        if (QL > 0) {
+#pragma unroll
+            for (int idx = 1; idx < R; idx++) {
+                const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                const uint32_t wi = (f * q) << (kStepTableLg - BS);
+                ZK_BOUND(wi, 1u << kStepTableLg);
+                tw[idx] = wtab[wi];
+            }
+        }
+        dft_small<RL, INV>(x[u]);
+        if (QL > 0) {
+#pragma unroll
+            for (int idx = 1; idx < R; idx++) x[u][idx] = gl_mul(x[u][idx], tw[idx]);
+        }
+        if (TO_GLOBAL) {
+            // QL == 0 here: base holds the leading digits, f the last one,
+            // which digit reversal moves to the top of i1.
+            const uint32_t i1b = digit_reverse<S>(base);
+            const uint64_t obase = l.out_base + (uint64_t)i1b * a.out_stride;
+#pragma unroll
+            for (int idx = 0; idx < R; idx++) {
+                const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                const uint32_t fi = f << (S - RL);
+                const uint32_t i1 = i1b + fi;
+                uint64_t val = x[u][idx];
+                if (ROLE == kRoleTable) {
+                    ZK_BOUND(i1, 1u << a.s);
+                    val = gl_mul(val, twtab[i1]);  // w_N^(i1 j2) for the tile's single j2
+                } else if (ROLE == kRoleTwiddle) {
+                    const uint64_t ex = (uint64_t)i1 * l.j2;
+                    if (ex) val = gl_mul(val, pass_root_pow(a, ex));
+                } else {
+                    if (ROLE == kRoleLastScale) val = gl_mul(val, a.scale);
+                    val = gl_canon(val);
+                }
+                const uint64_t oidx = obase + (uint64_t)fi * a.out_stride;
+                ZK_BOUND(oidx, a.out_len);
+                a.out[oidx] = val;
+            }
+        } else {
+            const uint32_t lbase = (base << logV) | v;
+#pragma unroll
+            for (int idx = 0; idx < R; idx++) {
+                const uint32_t f = bit_reverse((uint32_t)idx, RL);
+                const uint32_t li = lbase + ((f << QL) << logV);
+                ZK_BOUND(li, (1u << S) << logV);
+                lds[li] = x[u][idx];
+            }
+        }
+    }
+}
+
+// One radix-2^RL DIF step: every round of gather + finish.
+template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE, int LOGV>
+__host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, const PassLane& l,
+                                                  uint32_t tid, uint32_t T, uint64_t* lds, const uint64_t* wtab,
+                                                  const uint64_t* twtab)
+{
+    const uint32_t logV = LOGV >= 0 ? (uint32_t)LOGV : t.logV;
+    const uint32_t items = (1u << (S - RL)) << logV;
+    for (uint32_t it0 = tid; it0 < items; it0 += kStepU * T) {
+        uint64_t x[kStepU][1 << RL];
+        step_gather<S, RL, BS, KNZ, FROM_GLOBAL, LOGV>(a, t, l, it0, T, lds, x);
+        step_finish<S, RL, BS, INV, TO_GLOBAL, ROLE, LOGV>(a, t, l, it0, T, lds, wtab, twtab, x);
     }
 }
 
@@ -380,23 +423,43 @@ constexpr int pass_steps()
 // Whether the pass keeps a table of its inter-pass twiddles in LDS: a
 // multi-step, non-last pass whose tile holds a single j2 (J = 1). Then every
 // output i1 is multiplied by w_N^(i1 j2) with the same j2, and the 2^S powers
-// are formed once per workgroup after the tile (LDS words [2^S V, 2^S V + 2^S)).
+// are formed once per workgroup after the tile data (LDS words
+// [2^S V, 2^S V + 2^S)).
 __host__ __device__ __forceinline__ bool pass_uses_twtab(const PassArgs& a)
 {
     return a.s > 3 && !a.last && a.logJ == 0;
 }
 
-// Before step 0: fill the twiddle table (no barrier needed before step 0;
-// the table is read by the last step, after at least one barrier).
+// LDS words of a multi-step pass: the 2^S x V tile, the inter-pass twiddle
+// table (kRoleTable), then the step twiddles w_512^k (kW512Words).
+constexpr uint32_t kW512Words = 1u << kStepTableLg;
 template <int S, int ROLE>
-__host__ __device__ __forceinline__ void pass_prologue(const PassArgs& a, const PassTile& t,
-                                                       uint32_t tid, uint32_t T, uint64_t* lds)
+__host__ __device__ __forceinline__ uint32_t pass_wtab_offset(uint32_t logV)
 {
-    if (ROLE != kRoleTable) return;
+    return ((1u << S) << logV) + (ROLE == kRoleTable ? (1u << S) : 0u);
+}
+
+// Before step 0 (a barrier separates this from step 0, the first reader):
+// the step twiddles w_512^k into LDS and, for kRoleTable, the tile's
+// inter-pass twiddles w_N^(i1 j2) (read by the last step), in one loop so
+// that the global reads of both tables are in flight together.
+template <int S, int ROLE>
+__host__ __device__ __forceinline__ void pass_tables(const PassArgs& a, const PassTile& t, uint32_t tid,
+                                                     uint32_t T, uint64_t* lds)
+{
+    if (S <= 3) return;
+    uint64_t* wtab = lds + pass_wtab_offset<S, ROLE>(t.logV);
     uint64_t* tab = lds + ((1u << S) << t.logV);
-    for (uint32_t i = tid; i < (1u << S); i += T) {
-        const uint64_t ex = (uint64_t)i * t.j20;
-        tab[i] = ex ? pass_root_pow(a, ex) : 1;
+    constexpr uint32_t len = kW512Words > (1u << S) ? kW512Words : (1u << S);
+    for (uint32_t i = tid; i < len; i += T) {
+        const uint64_t w = i < kW512Words ? a.w512[i] : 0;
+        uint64_t tw = 1;
+        if (ROLE == kRoleTable && i < (1u << S)) {
+            const uint64_t ex = (uint64_t)i * t.j20;
+            if (ex) tw = pass_root_pow(a, ex);
+        }
+        if (i < kW512Words) wtab[i] = w;
+        if (ROLE == kRoleTable && i < (1u << S)) tab[i] = tw;
     }
 }
 
@@ -410,19 +473,42 @@ __host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, con
     using Rd = Radix<S>;
     constexpr int n = Rd::n;
     const uint64_t* tab = ROLE == kRoleTable ? lds + ((1u << S) << t.logV) : nullptr;
+    const uint64_t* wtab = lds + pass_wtab_offset<S, ROLE>(t.logV);
     if (k == 0) {
         if (n == 1)
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, true, ROLE, LOGV>(a, t, l, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, true, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr);
         else
-            ntt_step<S, Rd::r0, S, KNZ, INV, true, false, ROLE, LOGV>(a, t, l, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r0, S, KNZ, INV, true, false, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr);
     } else if (k == 1) {
         if (n == 2)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, tab);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, tab);
         else if (n == 3)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false, ROLE, LOGV>(a, t, l, tid, T, lds, nullptr);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr);
     } else if (k == 2) {
-        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, tab);
+        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, tab);
     }
+}
+
+// Step 0 of a multi-step pass in two halves, so that a kernel can issue its
+// HBM reads before the LDS tables are filled: the reads of all items (one
+// round: 2^(S - r0) V <= kStepU T) and, after a barrier, the rest.
+template <int S, int KNZ, int LOGV>
+__host__ __device__ __forceinline__ void pass_step0_gather(const PassArgs& a, const PassTile& t,
+                                                           const PassLane& l, uint32_t tid, uint32_t T,
+                                                           uint64_t (&x)[kStepU][1 << Radix<S>::r0])
+{
+    step_gather<S, Radix<S>::r0, S, KNZ, true, LOGV>(a, t, l, tid, T, nullptr, x);
+}
+
+template <int S, bool INV, int ROLE, int LOGV>
+__host__ __device__ __forceinline__ void pass_step0_finish(const PassArgs& a, const PassTile& t,
+                                                           const PassLane& l, uint32_t tid, uint32_t T,
+                                                           uint64_t* lds,
+                                                           uint64_t (&x)[kStepU][1 << Radix<S>::r0])
+{
+    static_assert(Radix<S>::n > 1, "a single-step pass writes HBM from step 0");
+    const uint64_t* wtab = lds + pass_wtab_offset<S, ROLE>(t.logV);
+    step_finish<S, Radix<S>::r0, S, INV, false, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr, x);
 }
 
 // Role of a pass (see PassRole).

@@ -147,12 +147,14 @@ inline bool plan_fits(const Plan& p, uint64_t w)
            (n >> p.sb[0]) * w < (1ull << 32);
 }
 
-// LDS of a pass: the N1 x V tile, unless the sub-DFT is a single step.
+// LDS of a pass: the N1 x V tile, the inter-pass twiddle table (kRoleTable)
+// and the step twiddles, unless the sub-DFT is a single step.
 inline size_t pass_lds_bytes(const PassArgs& a)
 {
     if (a.s <= 3) return 0;
     size_t words = (size_t)1 << (a.s + a.logC + a.logJ);
     if (pass_uses_twtab(a)) words += (size_t)1 << a.s;
+    words += kW512Words;
     return words * 8;
 }
 
