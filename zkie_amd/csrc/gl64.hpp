@@ -26,13 +26,32 @@ constexpr uint64_t INV_2_32 = 0xFFFFFFFE00000002ull;  // 2^-32 mod p
 
 __host__ __device__ __forceinline__ uint64_t gl_canon(uint64_t a) { return a >= P ? a - P : a; }
 
+// Rare corrections. Several reductions end in a correction that a lane needs
+// with probability about 2^-32 or less (a second wrap or borrow that only
+// operands near 2^64 can cause). On the device such a correction runs behind
+// a branch on the wave's mask of the lanes that need it: one scalar compare
+// and a branch that is almost never taken, instead of vector instructions in
+// every lane. On the host it is an ordinary conditional. Either way every
+// lane that needs the correction gets it.
+__host__ __device__ __forceinline__ bool any_lane(bool c)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_ballot_w64(c) != 0;
+#else
+    return c;
+#endif
+}
+#define ZK_RARE(c) __builtin_expect(any_lane(c), 0)
+
 // a + b for any a, b < 2^64.
 __host__ __device__ __forceinline__ uint64_t gl_add(uint64_t a, uint64_t b)
 {
     uint64_t s = a + b;
     uint64_t t = s + ((s < a) ? EPS : 0);
-    // A second wrap needs both operands above p; fold it the same way.
-    return t + ((t < s) ? EPS : 0);
+    // A second wrap needs both operands at least p: rare, folded the same way.
+    const bool w2 = t < s;
+    if (ZK_RARE(w2)) t += w2 ? EPS : 0;
+    return t;
 }
 
 // a + b where b < p (or any b <= 2^64 - 2^32): a single wrap at most.
@@ -47,7 +66,10 @@ __host__ __device__ __forceinline__ uint64_t gl_sub(uint64_t a, uint64_t b)
 {
     uint64_t d = a - b;
     uint64_t t = d - ((a < b) ? EPS : 0);
-    return t - ((t > d) ? EPS : 0);
+    // A second borrow needs b >= p + a: rare.
+    const bool b2 = t > d;
+    if (ZK_RARE(b2)) t -= b2 ? EPS : 0;
+    return t;
 }
 
 __host__ __device__ __forceinline__ uint64_t gl_neg(uint64_t a) { return gl_sub(0, a); }
@@ -80,8 +102,25 @@ __host__ __device__ __forceinline__ uint64_t gl_reduce128(uint64_t lo, uint64_t 
 //   a b = L + 2^64 H + 2^96 c = L + eps H.lo - H.hi - c   (2^64 = eps, 2^96 = -1).
 // S = L + eps H.lo wraps at most once (carry folds back as + eps, no second
 // wrap); S - H.hi - c borrows at most once (borrow folds back as - eps on a
-// value >= 2^64 - 2^32, no second borrow). A VALU write of an SGPR needs two
-// wait states before a VALU reads it as carry-in or lane mask (s_nop 1).
+// value >= 2^64 - 2^32, no second borrow). That borrow needs S < 2^32, i.e.
+// H.lo = 0 and L < 2^32, so it is a rare correction (gl_fix_borrow behind a
+// wave-uniform branch). A VALU write of an SGPR needs two wait states before a
+// VALU reads it as carry-in or lane mask (s_nop 1).
+
+// d -= eps in the lanes of mask k, where a borrow left d >= 2^64 - 2^32.
+__device__ __forceinline__ void gl_fix_borrow(uint32_t& d0, uint32_t& d1, uint64_t k)
+{
+    uint32_t e;
+    uint64_t kk;
+    asm("s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, -1, %4\n\t"
+        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
+        "s_nop 1\n\t"
+        "v_subb_co_u32_e64 %1, %3, %1, 0, %3"
+        : "+v"(d0), "+v"(d1), "=&v"(e), "=&s"(kk)
+        : "s"(k));
+}
+
 __device__ __forceinline__ uint64_t gl_mul_dev(uint64_t a, uint64_t b)
 {
     const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
@@ -100,18 +139,14 @@ __device__ __forceinline__ uint64_t gl_mul_dev(uint64_t a, uint64_t b)
         "v_mad_u64_u32 %0, %1, %2, -1, %0"
         : "=&v"(S), "=&s"(m1), "=&v"(c1)
         : "v"((uint32_t)H), "v"(L));
-    uint32_t d0, d1, e;
+    uint32_t d0, d1;
     uint64_t k;
-    asm("v_subb_co_u32_e64 %0, %3, %4, %6, %7\n\t"
+    asm("v_subb_co_u32_e64 %0, %2, %3, %5, %6\n\t"
         "s_nop 1\n\t"
-        "v_subb_co_u32_e64 %1, %3, %5, 0, %3\n\t"
-        "s_nop 1\n\t"
-        "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
-        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
-        "s_nop 1\n\t"
-        "v_subb_co_u32_e64 %1, %3, %1, 0, %3"
-        : "=&v"(d0), "=&v"(d1), "=&v"(e), "=&s"(k)
+        "v_subb_co_u32_e64 %1, %2, %4, 0, %2"
+        : "=&v"(d0), "=&v"(d1), "=&s"(k)
         : "v"((uint32_t)S), "v"((uint32_t)(S >> 32)), "v"((uint32_t)(H >> 32)), "s"(m));
+    if (__builtin_expect(k != 0, 0)) gl_fix_borrow(d0, d1, k);
     return ((uint64_t)d1 << 32) | d0;
 }
 #endif
@@ -182,23 +217,19 @@ __host__ __device__ __forceinline__ void gl_mul2(uint64_t a, uint64_t b, uint64_
         "v_mad_u64_u32 %1, %3, %5, -1, %1"
         : "=&v"(Sa), "=&v"(Sb), "=&s"(ka), "=&s"(kb), "=&v"(ca), "=&v"(cb)
         : "v"((uint32_t)Ha), "v"(La), "v"((uint32_t)Hb), "v"(Lb));
-    uint32_t xa0, xa1, xb0, xb1, ea, eb;
-    asm("v_subb_co_u32_e64 %0, %6, %8, %10, %11\n\t"
-        "v_subb_co_u32_e64 %2, %7, %12, %14, %15\n\t"
+    uint32_t xa0, xa1, xb0, xb1;
+    asm("v_subb_co_u32_e64 %0, %4, %6, %8, %9\n\t"
+        "v_subb_co_u32_e64 %2, %5, %10, %12, %13\n\t"
         "s_nop 0\n\t"
-        "v_subb_co_u32_e64 %1, %6, %9, 0, %6\n\t"
-        "v_subb_co_u32_e64 %3, %7, %13, 0, %7\n\t"
-        "s_nop 0\n\t"
-        "v_cndmask_b32_e64 %4, 0, -1, %6\n\t"
-        "v_cndmask_b32_e64 %5, 0, -1, %7\n\t"
-        "v_sub_co_u32_e64 %0, %6, %0, %4\n\t"
-        "v_sub_co_u32_e64 %2, %7, %2, %5\n\t"
-        "s_nop 0\n\t"
-        "v_subb_co_u32_e64 %1, %6, %1, 0, %6\n\t"
-        "v_subb_co_u32_e64 %3, %7, %3, 0, %7"
-        : "=&v"(xa0), "=&v"(xa1), "=&v"(xb0), "=&v"(xb1), "=&v"(ea), "=&v"(eb), "=&s"(ka), "=&s"(kb)
+        "v_subb_co_u32_e64 %1, %4, %7, 0, %4\n\t"
+        "v_subb_co_u32_e64 %3, %5, %11, 0, %5"
+        : "=&v"(xa0), "=&v"(xa1), "=&v"(xb0), "=&v"(xb1), "=&s"(ka), "=&s"(kb)
         : "v"((uint32_t)Sa), "v"((uint32_t)(Sa >> 32)), "v"((uint32_t)(Ha >> 32)), "s"(ma),
           "v"((uint32_t)Sb), "v"((uint32_t)(Sb >> 32)), "v"((uint32_t)(Hb >> 32)), "s"(mb));
+    if (__builtin_expect((ka | kb) != 0, 0)) {
+        gl_fix_borrow(xa0, xa1, ka);
+        gl_fix_borrow(xb0, xb1, kb);
+    }
     x = ((uint64_t)xa1 << 32) | xa0;
     y = ((uint64_t)xb1 << 32) | xb0;
 #else
@@ -235,7 +266,8 @@ __host__ __device__ __forceinline__ uint64_t gl_sub_small(uint64_t a, uint64_t b
 }
 
 // a - b for any a, b: the first borrow folds back as - eps, which borrows
-// again only when a - b + 2^64 < eps; the third subtraction cannot borrow.
+// again only when a - b + 2^64 < eps, i.e. b >= p + a (rare: gl_fix_borrow
+// behind a wave-uniform branch); the third subtraction cannot borrow.
 __host__ __device__ __forceinline__ uint64_t gl_sub2(uint64_t a, uint64_t b)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
@@ -248,14 +280,10 @@ __host__ __device__ __forceinline__ uint64_t gl_sub2(uint64_t a, uint64_t b)
         "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
         "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
         "s_nop 1\n\t"
-        "v_subb_co_u32_e64 %1, %3, %1, 0, %3\n\t"
-        "s_nop 1\n\t"
-        "v_cndmask_b32_e64 %2, 0, -1, %3\n\t"
-        "v_sub_co_u32_e64 %0, %3, %0, %2\n\t"
-        "s_nop 1\n\t"
         "v_subb_co_u32_e64 %1, %3, %1, 0, %3"
         : "=&v"(d0), "=&v"(d1), "=&v"(e), "=&s"(k)
         : "v"((uint32_t)a), "v"((uint32_t)(a >> 32)), "v"((uint32_t)b), "v"((uint32_t)(b >> 32)));
+    if (__builtin_expect(k != 0, 0)) gl_fix_borrow(d0, d1, k);
     return ((uint64_t)d1 << 32) | d0;
 #else
     return gl_sub(a, b);
@@ -275,6 +303,29 @@ __host__ __device__ __forceinline__ uint64_t gl_add_meps(uint64_t s, uint32_t m)
         "v_mad_u64_u32 %0, %1, %2, -1, %0"
         : "=&v"(S), "=&s"(k), "=&v"(c)
         : "v"(m), "v"(s));
+    return S;
+#else
+    return gl_add(s, (uint64_t)m * EPS);
+#endif
+}
+
+// s + m eps where the product-add rarely wraps (m eps far below 2^64 - s,
+// e.g. m a small count of wraps): the wrap folds back behind a
+// wave-uniform branch.
+__host__ __device__ __forceinline__ uint64_t gl_add_meps_rare(uint64_t s, uint32_t m)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint64_t S, k;
+    asm("v_mad_u64_u32 %0, %1, %2, -1, %3" : "=&v"(S), "=s"(k) : "v"(m), "v"(s));
+    if (__builtin_expect(k != 0, 0)) {
+        uint64_t kk;
+        uint32_t c;
+        asm("s_nop 1\n\t"
+            "v_cndmask_b32_e64 %1, 0, 1, %3\n\t"
+            "v_mad_u64_u32 %0, %2, %1, -1, %0"
+            : "+v"(S), "=&v"(c), "=&s"(kk)
+            : "s"(k));
+    }
     return S;
 #else
     return gl_add(s, (uint64_t)m * EPS);
@@ -321,7 +372,8 @@ __host__ __device__ __forceinline__ uint64_t acc32s(uint64_t acc, uint32_t x)
 
 // A + B 2^32 mod p for A, B < 2^63 (sums of 32-bit halves): with
 // t = A + (B.lo << 32) and its carry c, the value is t + (B.hi + c) 2^64
-// and 2^64 = eps.
+// and 2^64 = eps. For the sums of a linear layer B.hi + c is a small count,
+// so the final fold is a rare correction.
 __host__ __device__ __forceinline__ uint64_t gl_from_halves(uint64_t A, uint64_t B)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
@@ -332,7 +384,7 @@ __host__ __device__ __forceinline__ uint64_t gl_from_halves(uint64_t A, uint64_t
         "v_addc_co_u32_e64 %1, %2, %5, 0, %2"
         : "=&v"(th), "=&v"(k), "=&s"(m)
         : "v"((uint32_t)(A >> 32)), "v"((uint32_t)B), "v"((uint32_t)(B >> 32)));
-    return gl_add_meps(((uint64_t)th << 32) | (uint32_t)A, k);
+    return gl_add_meps_rare(((uint64_t)th << 32) | (uint32_t)A, k);
 #else
     const uint64_t t = A + (B << 32);
     const uint32_t k = (uint32_t)(B >> 32) + (t < A ? 1u : 0u);
@@ -367,11 +419,13 @@ __host__ __device__ __forceinline__ uint64_t gl_mul_2e48(uint64_t x)
     return gl_sub_small(gl_add_meps(x << 48, (uint32_t)hi), hi >> 32);
 }
 
-// Canonical representative: x >= p exactly when x + eps wraps.
+// Canonical representative of a value that is rarely >= p (x - p = x + eps
+// mod 2^64, behind a wave-uniform branch).
 __host__ __device__ __forceinline__ uint64_t gl_canon_fast(uint64_t x)
 {
-    const uint64_t t = x + EPS;
-    return t < x ? t : x;
+    const bool big = x >= P;
+    if (ZK_RARE(big)) x = big ? x + EPS : x;
+    return x;
 }
 
 // x * 2^S for S in {1, 2}: lo + k 2^64 with k < 2^S, and k eps < p folds in
@@ -381,8 +435,10 @@ __host__ __device__ __forceinline__ uint64_t gl_shl(uint64_t x)
 {
     static_assert(S >= 1 && S <= 2, "shift range");
     const uint64_t lo = x << S;
-    const uint64_t r = lo + (x >> (64 - S)) * EPS;
-    return r + (r < lo ? EPS : 0);
+    uint64_t r = lo + (x >> (64 - S)) * EPS;
+    const bool w = r < lo;  // rare: lo within 3 eps of 2^64
+    if (ZK_RARE(w)) r += w ? EPS : 0;
+    return r;
 }
 
 // sum + x * 2^S for S in {1, 2}: the two wraps (shifted-out bits and the
@@ -393,8 +449,10 @@ __host__ __device__ __forceinline__ uint64_t gl_add_shl(uint64_t sum, uint64_t x
     static_assert(S >= 1 && S <= 2, "shift range");
     const uint64_t lo = (x << S) + sum;
     const uint64_t k = (x >> (64 - S)) + (lo < sum ? 1 : 0);
-    const uint64_t r = lo + k * EPS;
-    return r + (r < lo ? EPS : 0);
+    uint64_t r = lo + k * EPS;
+    const bool w = r < lo;  // rare: lo within 5 eps of 2^64
+    if (ZK_RARE(w)) r += w ? EPS : 0;
+    return r;
 }
 
 __host__ __device__ __forceinline__ uint64_t gl_halve(uint64_t x)

@@ -144,7 +144,7 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
     // sum = slo + shi 2^32 = slo + (shi.lo << 32) + shi.hi 2^64, and 2^64 = eps
     const uint64_t t = slo + (shi << 32);
     const uint32_t k = (uint32_t)(shi >> 32) + (t < slo ? 1u : 0u);
-    const uint64_t sum = gl_canon_fast(gl_add_meps(t, k));
+    const uint64_t sum = gl_canon_fast(gl_add_meps_rare(t, k));
 
     const uint64_t x15 = st[15];
     st[0] = gl_sub2(sum, gl_shl<1>(x0));                                   // -2
