@@ -11,12 +11,15 @@
 //  * round constants sit in __constant__ memory indexed by wave-uniform
 //    loop counters, so the compiler reads them with scalar loads into SGPRs
 //    and every VALU op takes them as a scalar operand;
-//  * the linear layers accumulate into a lazy 96-bit sum (Acc) and reduce
-//    once per output, instead of reducing after every addition, and the next
-//    round's constants are folded into that same reduction;
+//  * the linear layers work on the 32-bit halves of the state as exact
+//    64-bit sums (one v_mad_u64_u32 per term) and reduce once per output,
+//    folding the next round's constants into that same reduction;
+//  * corrections that a lane needs only with probability about 2^-32 (the
+//    multiply's final borrow, second wraps, the linear-layer folds) run
+//    behind wave-uniform branches (gl64.hpp);
 //  * 1/2^k multiplies are shift/add sequences (gl_mul_inv_pow2), and the
-//    2^-32 entry uses the same closed form when diag15 has that value; 2x,
-//    3x and 4x are shifts with the wrapped bits folded back once;
+//    2^-32 entry uses a closed form when diag15 has that value; 2x, 3x and
+//    4x are shifts with the wrapped bits folded back once;
 //  * in the internal rounds the work that does not depend on the S-box is
 //    issued before it, and the round sum is made canonical so the sixteen
 //    "sum + t" additions need one wrap correction each;
@@ -52,23 +55,9 @@ __host__ __device__ __forceinline__ void sbox7_2(uint64_t& x, uint64_t& y)
     gl_mul2(x3, x4, y3, y4, x, y);
 }
 
-// mat4 = [2 3 1 1; 1 2 3 1; 1 1 2 3; 3 1 1 2] on lazy sums
-// (addition chain of poseidon2_merkle.cu:63-76).
-__host__ __device__ __forceinline__ void mat4_lazy(const uint64_t* x, Acc* y)
-{
-    const Acc t01 = acc_add(acc_of(x[0]), x[1]);
-    const Acc t23 = acc_add(acc_of(x[2]), x[3]);
-    const Acc t0123 = acc_add(t01, t23);
-    const Acc t01123 = acc_add(t0123, x[1]);
-    const Acc t01233 = acc_add(t0123, x[3]);
-    y[3] = acc_add(acc_add(t01233, x[0]), x[0]);  // 3x0 + x1 + x2 + 2x3
-    y[1] = acc_add(acc_add(t01123, x[2]), x[2]);  // x0 + 2x1 + 3x2 + x3
-    y[0] = acc_add(t01123, t01);                  // 2x0 + 3x1 + x2 + x3
-    y[2] = acc_add(t01233, t23);                  // x0 + x1 + 2x2 + 3x3
-}
-
-// mat4 on one 32-bit half of four lanes, into 64-bit sums (coefficients
-// 1, 2, 3, so no sum can carry).
+// mat4 = [2 3 1 1; 1 2 3 1; 1 1 2 3; 3 1 1 2] (the addition chain of
+// poseidon2_merkle.cu:63-76) on one 32-bit half of four lanes, into 64-bit
+// sums (coefficients 1, 2, 3, so no sum can carry).
 __host__ __device__ __forceinline__ void mat4_half(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
                                                    uint64_t* y)
 {
@@ -83,40 +72,56 @@ __host__ __device__ __forceinline__ void mat4_half(uint32_t x0, uint32_t x1, uin
     y[2] = t01233 + t23;           // x0 + x1 + 2x2 + 3x3
 }
 
-// mat4 of each lane group on one half, and the column sums
-// sums[k] = sum_g y_{4g + k}; output i is then y_i + sums[i mod 4].
-template <bool HI>
-__host__ __device__ __forceinline__ void mds_half(const uint64_t* st, uint64_t* y, uint64_t* sums)
+// mat4 on 64-bit sums (used on the column sums of the four lane groups).
+__host__ __device__ __forceinline__ void mat4_wide(const uint64_t* x, uint64_t* y)
 {
-#pragma unroll
-    for (int j = 0; j < 16; j += 4) {
-        if (HI)
-            mat4_half((uint32_t)(st[j] >> 32), (uint32_t)(st[j + 1] >> 32), (uint32_t)(st[j + 2] >> 32),
-                      (uint32_t)(st[j + 3] >> 32), y + j);
-        else
-            mat4_half((uint32_t)st[j], (uint32_t)st[j + 1], (uint32_t)st[j + 2], (uint32_t)st[j + 3], y + j);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) sums[k] = (y[k] + y[4 + k]) + (y[8 + k] + y[12 + k]);
+    const uint64_t t01 = x[0] + x[1];
+    const uint64_t t23 = x[2] + x[3];
+    const uint64_t t0123 = t01 + t23;
+    const uint64_t t01123 = t0123 + x[1];
+    const uint64_t t01233 = t0123 + x[3];
+    y[3] = t01233 + (x[0] << 1);  // 3x0 + x1 + x2 + 2x3
+    y[1] = t01123 + (x[2] << 1);  // x0 + 2x1 + 3x2 + x3
+    y[0] = t01123 + t01;          // 2x0 + 3x1 + x2 + x3
+    y[2] = t01233 + t23;          // x0 + x1 + 2x2 + 3x3
 }
 
-// st <- mds_light16(st) (+ rc if given). Both 32-bit halves of the state go
-// through the layer as exact 64-bit sums (at most 35 (2^32 - 1) + 2^32 each),
-// and each output is reduced once from its two sums as it is formed.
+// st <- mds_light16(st) (+ rc if given). Output 4g + k is mat4(x_g)[k] +
+// sum_h mat4(x_h)[k], and the column sum equals mat4(sum_h x_h)[k] (mat4
+// is linear), so the sums come from the four-lane group sums first and each
+// group is then transformed and written on its own: only one group's
+// intermediate sums are live at a time. Both 32-bit halves of the state go
+// through the layer as exact 64-bit sums (at most 35 (2^32 - 1) + 2^32
+// each), and each output is reduced once from its two sums.
 template <bool ADD_RC>
 __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_t* rc)
 {
-    uint64_t ylo[16], yhi[16], slo[4], shi[4];
-    mds_half<false>(st, ylo, slo);
-    mds_half<true>(st, yhi, shi);
+    uint64_t gl[4], gh[4], sl[4], sh[4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        uint64_t A = ylo[i] + slo[i & 3], B = yhi[i] + shi[i & 3];
-        if (ADD_RC) {
-            A = acc32s(A, (uint32_t)rc[i]);
-            B = acc32s(B, (uint32_t)(rc[i] >> 32));
+    for (int k = 0; k < 4; k++) {
+        gl[k] = acc32(acc32(acc32m<1>((uint32_t)st[k], (uint32_t)st[4 + k]), (uint32_t)st[8 + k]),
+                      (uint32_t)st[12 + k]);
+        gh[k] = acc32(acc32(acc32m<1>((uint32_t)(st[k] >> 32), (uint32_t)(st[4 + k] >> 32)),
+                            (uint32_t)(st[8 + k] >> 32)),
+                      (uint32_t)(st[12 + k] >> 32));
+    }
+    mat4_wide(gl, sl);
+    mat4_wide(gh, sh);
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) {
+        uint64_t yl[4], yh[4];
+        mat4_half((uint32_t)st[j], (uint32_t)st[j + 1], (uint32_t)st[j + 2], (uint32_t)st[j + 3], yl);
+        mat4_half((uint32_t)(st[j] >> 32), (uint32_t)(st[j + 1] >> 32), (uint32_t)(st[j + 2] >> 32),
+                  (uint32_t)(st[j + 3] >> 32), yh);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint64_t A = yl[k] + sl[k], B = yh[k] + sh[k];
+            if (ADD_RC) {
+                A = acc32s(A, (uint32_t)rc[j + k]);
+                B = acc32s(B, (uint32_t)(rc[j + k] >> 32));
+            }
+            st[j + k] = gl_from_halves(A, B);
         }
-        st[i] = gl_from_halves(A, B);
     }
 }
 
