@@ -131,6 +131,12 @@ uint64_t emu_acc_sum(const uint64_t* x, uint64_t n)
     return acc_reduce(a);
 }
 uint64_t emu_gl_canon(uint64_t a) { return gl_canon(a); }
+uint64_t emu_dot(const uint64_t* e, const uint64_t* x, uint64_t n)
+{
+    DotAcc d;
+    for (uint64_t i = 0; i < n; i++) dot_add(d, e[i], x[i]);
+    return gl_canon(dot_reduce(d));
+}
 uint64_t emu_gl_canon_fast(uint64_t a) { return gl_canon_fast(a); }
 uint64_t emu_gl_shl(uint64_t a, int s) { return s == 1 ? gl_shl<1>(a) : gl_shl<2>(a); }
 uint64_t emu_gl_add_shl(uint64_t sum, uint64_t a, int s)

@@ -45,6 +45,8 @@ def load():
             getattr(L, n).argtypes = [_u64]
         L.emu_gl_inv_pow2.restype = _u64
         L.emu_gl_inv_pow2.argtypes = [_u64, ctypes.c_int]
+        L.emu_dot.restype = _u64
+        L.emu_dot.argtypes = [_u64p, _u64p, _u64]
         L.emu_acc_sum.restype = _u64
         L.emu_acc_sum.argtypes = [_u64p, _u64]
         L.emu_p2_permute.argtypes = [_u64p, _u64p, _u64p, _u64p, _u64, ctypes.c_int]

@@ -37,6 +37,21 @@ def test_arithmetic(emu):
         assert emu.emu_gl_canon(emu.emu_acc_sum(ptr(x), n)) == sum(int(v) for v in x) % P
 
 
+def test_dot_accumulator(emu):
+    """DotAcc (exact 32 x 32 partial-product sums, one reduction) against
+    python integers, with all-ones operands that force every carry."""
+    import random
+    rng = random.Random(5)
+    cases = [[(2**64 - 1, 2**64 - 1)] * 128, [(2**64 - 1, P - 1)] * 65, [(0, 5)] * 3, []]
+    for n in (1, 2, 16, 64, 128):
+        cases.append([(rng.getrandbits(64), rng.getrandbits(64)) for _ in range(n)])
+    for pairs in cases:
+        e = np.array([a for a, _ in pairs] or [0], np.uint64)
+        x = np.array([b for _, b in pairs] or [0], np.uint64)
+        want = sum(a * b for a, b in pairs) % P
+        assert emu.emu_dot(ptr(e), ptr(x), len(pairs)) == want
+
+
 @pytest.mark.parametrize("fast", [0, 1])
 def test_permutation(emu, oracle, fast):
     a, b, c, d = oracle.p2_constants()

@@ -7,7 +7,9 @@
 // applied to the table viewed as 2^(n-k) rows of 2^k, the table fold over
 // the low k variables (mle.rs:25-38 partial_eval).
 // One row per lane; the 2^k eq weights are computed once on the host and
-// read as wave-uniform values; the codeword is streamed exactly once.
+// read as wave-uniform values; each output is an exact dot product of the
+// row with the weights (DotAcc: 32 x 32 partial products, one reduction per
+// output); the codeword is streamed exactly once.
 #include <vector>
 
 #include "gl64.hpp"
@@ -20,9 +22,9 @@ namespace {
 // eq weights of a fold with k <= 6 (at most 64 EF values), passed by value
 // as a kernel argument: they reach the kernel as scalar loads from the
 // argument segment, and no device buffer has to outlive the launch, so the
-// call does not synchronise its stream.
+// call does not synchronise its stream. Entry j is [e.c0, e.c1, 7 e.c1].
 struct EqArg {
-    uint64_t v[128];
+    uint64_t v[192];
 };
 
 template <int K, bool EXT>
@@ -48,26 +50,26 @@ __global__ __launch_bounds__(256) void fold_kernel(const uint64_t* __restrict__ 
         if (t >= h) return;
         row = mat + t * RW;
     }
-    Acc s0 = acc_of(0), s1 = acc_of(0);
+    // (e0 + e1 x)(y0 + y1 x) = (e0 y0 + 7 e1 y1) + (e0 y1 + e1 y0) x
+    DotAcc s0, s1;
     if (!EXT) {
 #pragma unroll
         for (int j = 0; j < Wd; j++) {
             const uint64_t x = row[j];
-            s0 = acc_add(s0, gl_mul(eq[2 * j + 0], x));
-            s1 = acc_add(s1, gl_mul(eq[2 * j + 1], x));
+            dot_add(s0, eq[3 * j], x);
+            dot_add(s1, eq[3 * j + 1], x);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < Wd; j++) {
             const uint64_t y0 = row[2 * j], y1 = row[2 * j + 1];
-            const uint64_t e0 = eq[2 * j], e1 = eq[2 * j + 1];
-            s0 = acc_add(s0, gl_mul(e0, y0));
-            s0 = acc_add(s0, gl_mul7(gl_mul(e1, y1)));
-            s1 = acc_add(s1, gl_mul(e0, y1));
-            s1 = acc_add(s1, gl_mul(e1, y0));
+            dot_add(s0, eq[3 * j], y0);
+            dot_add(s0, eq[3 * j + 2], y1);
+            dot_add(s1, eq[3 * j], y1);
+            dot_add(s1, eq[3 * j + 1], y0);
         }
     }
-    reinterpret_cast<ulonglong2*>(out)[t] = make_ulonglong2(gl_canon(acc_reduce(s0)), gl_canon(acc_reduce(s1)));
+    reinterpret_cast<ulonglong2*>(out)[t] = make_ulonglong2(gl_canon(dot_reduce(s0)), gl_canon(dot_reduce(s1)));
 }
 
 // Generic width (K > 6): runtime loop.
@@ -125,7 +127,11 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
     const unsigned grid = (unsigned)((h + 255) / 256);
     if (k <= 6) {
         EqArg ea{};
-        for (size_t i = 0; i < eq.size(); i++) ea.v[i] = eq[i];
+        for (size_t j = 0; 2 * j < eq.size(); j++) {
+            ea.v[3 * j] = eq[2 * j];
+            ea.v[3 * j + 1] = eq[2 * j + 1];
+            ea.v[3 * j + 2] = gl_canon(gl_mul7(eq[2 * j + 1]));
+        }
         ProfMark m = prof_begin("fold_rows", s);
 #define ZK_FOLD(KK)                                                                  \
     case KK:                                                                         \

@@ -500,6 +500,68 @@ __host__ __device__ __forceinline__ uint64_t acc_reduce(Acc a)
     return gl_add_small(a.lo, t);
 }
 
+// Exact running sum of products e * x, e wave-uniform (on the device it is
+// taken as a scalar operand, so it must be the same in every lane) and x per
+// lane, for
+// dot products that are reduced once at the end: the four 32 x 32 partial
+// products accumulate in three 64-bit sums with carry counts,
+//   sum = a0 + a1 2^32 + a2 2^64 + c0 2^64 + c1 2^96 + c2 2^128,
+// 8 VALU instructions per term instead of a reduced multiply and addition.
+// The counts stay below 2^32 for up to 2^31 terms.
+struct DotAcc {
+    uint64_t a0 = 0, a1 = 0, a2 = 0;
+    uint32_t c0 = 0, c1 = 0, c2 = 0;
+};
+
+__host__ __device__ __forceinline__ void dot_add(DotAcc& d, uint64_t e, uint64_t x)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    const uint32_t el = (uint32_t)e, eh = (uint32_t)(e >> 32);
+    const uint32_t xl = (uint32_t)x, xh = (uint32_t)(x >> 32);
+    uint64_t k0, k1, k2, k3, kx;
+    // each carry mask is read at least two instructions after its write
+    asm("v_mad_u64_u32 %0, %6, %11, %13, %0\n\t"
+        "v_mad_u64_u32 %1, %7, %12, %13, %1\n\t"
+        "v_mad_u64_u32 %2, %9, %12, %14, %2\n\t"
+        "v_mad_u64_u32 %1, %8, %11, %14, %1\n\t"
+        "v_addc_co_u32_e64 %3, %10, %3, 0, %6\n\t"
+        "v_addc_co_u32_e64 %4, %10, %4, 0, %7\n\t"
+        "v_addc_co_u32_e64 %5, %10, %5, 0, %9\n\t"
+        "v_addc_co_u32_e64 %4, %10, %4, 0, %8"
+        : "+v"(d.a0), "+v"(d.a1), "+v"(d.a2), "+v"(d.c0), "+v"(d.c1), "+v"(d.c2), "=&s"(k0), "=&s"(k1),
+          "=&s"(k2), "=&s"(k3), "=&s"(kx)
+        : "v"(xl), "v"(xh), "s"(el), "s"(eh));
+#else
+    const uint64_t el = e & 0xFFFFFFFFull, eh = e >> 32, xl = x & 0xFFFFFFFFull, xh = x >> 32;
+    uint64_t p = xl * el;
+    d.a0 += p;
+    d.c0 += d.a0 < p ? 1u : 0u;
+    p = xh * el;
+    d.a1 += p;
+    d.c1 += d.a1 < p ? 1u : 0u;
+    p = xh * eh;
+    d.a2 += p;
+    d.c2 += d.a2 < p ? 1u : 0u;
+    p = xl * eh;
+    d.a1 += p;
+    d.c1 += d.a1 < p ? 1u : 0u;
+#endif
+}
+
+// The accumulated sum mod p: with lo = a0 + (a1 << 32) and its carry, and
+// mid = (a1 >> 32) + a2 + c0 + carry (its own carry counted into the
+// 2^128 term), sum = lo + mid 2^64 + c1 2^96 + c2' 2^128, and 2^64 = eps,
+// 2^96 = -1, 2^128 = -2^32 give lo + mid.lo eps - (mid.hi + c1 + c2' 2^32).
+__host__ __device__ __forceinline__ uint64_t dot_reduce(const DotAcc& d)
+{
+    const uint64_t lo = d.a0 + (d.a1 << 32);
+    const uint64_t t = (d.a1 >> 32) + d.c0 + (lo < d.a0 ? 1u : 0u);
+    const uint64_t mid = d.a2 + t;
+    const uint64_t c2 = (uint64_t)d.c2 + (mid < t ? 1u : 0u);
+    const uint64_t q = (mid >> 32) + d.c1 + (c2 << 32);  // < p for counts below 2^31
+    return gl_sub_small(gl_add_meps(lo, (uint32_t)mid), q);
+}
+
 // Quadratic extension EF = F[x]/(x^2 - 7).
 struct Ef {
     uint64_t c0, c1;
