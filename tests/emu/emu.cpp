@@ -164,6 +164,24 @@ void emu_p2_permute(uint64_t* st, const uint64_t* rc_init, const uint64_t* rc_fi
     for (int i = 0; i < 16; i++) st[i] = gl_canon(st[i]);
 }
 
+// One internal round of the device code (st0 <- (st0 + rc)^7, then the
+// internal linear layer), canonical outputs.
+void emu_p2_internal_round(uint64_t* st, uint64_t rc, uint64_t diag15, int fast_diag)
+{
+    if (fast_diag)
+        internal_round<true>(st, rc, diag15);
+    else
+        internal_round<false>(st, rc, diag15);
+    for (int i = 0; i < 16; i++) st[i] = gl_canon(st[i]);
+}
+
+// One external linear layer (mds_light16, no constants), canonical outputs.
+void emu_p2_mds_light(uint64_t* st)
+{
+    mds_light16<false>(st, nullptr);
+    for (int i = 0; i < 16; i++) st[i] = gl_canon(st[i]);
+}
+
 // DFT (in place) / LDE through the device pass code. Returns 0 on success.
 int emu_dft(uint64_t* mat, uint32_t lg, uint64_t w, int inverse, uint32_t threads)
 {

@@ -50,6 +50,8 @@ def load():
         L.emu_acc_sum.restype = _u64
         L.emu_acc_sum.argtypes = [_u64p, _u64]
         L.emu_p2_permute.argtypes = [_u64p, _u64p, _u64p, _u64p, _u64, ctypes.c_int]
+        L.emu_p2_internal_round.argtypes = [_u64p, _u64, _u64, ctypes.c_int]
+        L.emu_p2_mds_light.argtypes = [_u64p]
         L.emu_dft.argtypes = [_u64p, ctypes.c_uint32, _u64, ctypes.c_int, ctypes.c_uint32]
         L.emu_dft.restype = ctypes.c_int
         L.emu_lde.argtypes = [_u64p, _u64, _u64, ctypes.c_uint32, _u64p, ctypes.c_uint32]

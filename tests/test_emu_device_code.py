@@ -69,6 +69,43 @@ def test_permutation(emu, oracle, fast):
     assert (s == oracle.p2_permute(np.arange(16, dtype=np.uint64))).all()
 
 
+def _edge_states(rng):
+    """States that hit the ends of every lane form: all-ones words, values
+    at and above p, halves of 0 and 2^32 - 1, powers of two, random."""
+    edge = [0, 1, 2, P - 1, P, P + 1, 2**64 - 1, 2**64 - 2, 2**32 - 1, 2**32, 2**63, 2**63 - 1,
+            0xFFFFFFFF00000000, 0x00000000FFFFFFFF, 0xFFFFFFFE00000002, 7, 2**31]
+    states = [[v] * 16 for v in edge]
+    for _ in range(40):
+        states.append([rng.choice(edge) if rng.random() < 0.5 else rng.getrandbits(64) for _ in range(16)])
+    return states
+
+
+@pytest.mark.parametrize("fast", [0, 1])
+def test_internal_round_edges(emu, oracle, fast):
+    """The internal round's lane forms (halves sums, complements, 2^-k splits)
+    against the oracle's round on edge states, including non-canonical input."""
+    import random
+    rng = random.Random(11 + fast)
+    a, b, c, d = oracle.p2_constants()
+    for st in _edge_states(rng):
+        for rc in (0, 1, P - 1, int(c[5])):
+            s = np.array(st, np.uint64)
+            emu.emu_p2_internal_round(ptr(s), rc, d, fast)
+            ref = np.array([v % P for v in st], np.uint64)
+            ref[0] = pow((int(ref[0]) + rc) % P, 7, P)
+            ref = oracle.p2_internal_linear(ref)
+            assert (s == ref).all(), (st, rc)
+
+
+def test_mds_light_edges(emu, oracle):
+    import random
+    rng = random.Random(13)
+    for st in _edge_states(rng):
+        s = np.array(st, np.uint64)
+        emu.emu_p2_mds_light(ptr(s))
+        assert (s == oracle.p2_mds_light(np.array([v % P for v in st], np.uint64))).all(), st
+
+
 @pytest.mark.parametrize("lg,w", [(1, 1), (3, 1), (5, 3), (9, 16), (10, 1), (10, 16), (12, 5),
                                   (14, 32), (16, 8), (19, 1), (18, 16), (13, 128)])
 def test_dft_passes(emu, oracle, lg, w):

@@ -392,6 +392,48 @@ __host__ __device__ __forceinline__ uint64_t gl_from_halves(uint64_t A, uint64_t
 #endif
 }
 
+// gl_from_halves without its final fold: returns A + B 2^32 folded once, and
+// w (device) the mask of the lanes in which the fold's product-add wrapped
+// and + eps is still due (gl_fold_eps), so that several outputs can share
+// one rare-correction branch. On the host the value is complete and w = 0.
+__host__ __device__ __forceinline__ uint64_t gl_from_halves_defer(uint64_t A, uint64_t B, uint64_t& w)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint32_t th, k;
+    uint64_t m, S;
+    asm("v_add_co_u32_e64 %0, %2, %3, %4\n\t"
+        "s_nop 1\n\t"
+        "v_addc_co_u32_e64 %1, %2, %5, 0, %2"
+        : "=&v"(th), "=&v"(k), "=&s"(m)
+        : "v"((uint32_t)(A >> 32)), "v"((uint32_t)B), "v"((uint32_t)(B >> 32)));
+    asm("v_mad_u64_u32 %0, %1, %2, -1, %3"
+        : "=&v"(S), "=s"(w)
+        : "v"(k), "v"(((uint64_t)th << 32) | (uint32_t)A));
+    return S;
+#else
+    w = 0;
+    return gl_from_halves(A, B);
+#endif
+}
+
+// r += eps in the lanes of mask w (a product-add of at most 2^32 eps wrapped
+// there, so the value is below 2^64 - 2^33 and + eps cannot wrap again).
+__host__ __device__ __forceinline__ void gl_fold_eps(uint64_t& r, uint64_t w)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint64_t kk;
+    uint32_t c;
+    asm("s_nop 1\n\t"
+        "v_cndmask_b32_e64 %1, 0, 1, %3\n\t"
+        "v_mad_u64_u32 %0, %2, %1, -1, %0"
+        : "+v"(r), "=&v"(c), "=&s"(kk)
+        : "s"(w));
+#else
+    (void)r;
+    (void)w;
+#endif
+}
+
 // x * 2^-k for 1 <= k <= 32, any x < 2^64:
 // x = q 2^k + r, r 2^-k = -r 2^(96-k) = -(m * eps) with m = r 2^(32-k) < 2^32,
 // and -(m * eps) = p - m 2^32 + m = (2^32 - 1 - m) 2^32 + (m + 1).

@@ -17,9 +17,10 @@
 //  * corrections that a lane needs only with probability about 2^-32 (the
 //    multiply's final borrow, second wraps, the linear-layer folds) run
 //    behind wave-uniform branches (gl64.hpp);
-//  * 1/2^k multiplies are shift/add sequences (gl_mul_inv_pow2), and the
-//    2^-32 entry uses a closed form when diag15 has that value; 2x, 3x and
-//    4x are shifts with the wrapped bits folded back once;
+//  * the internal diagonal is applied without multiplies: 2^-k splits x
+//    into x >> k and the shifted-out bits, the 2^-32 entry uses a closed form
+//    when diag15 has that value, and 2x, 3x, 4x, -3x are exact sums of
+//    halves or shifts with the wrapped bits folded back once;
 //  * in the internal rounds the work that does not depend on the S-box is
 //    issued before it, and the round sum is made canonical so the sixteen
 //    "sum + t" additions need one wrap correction each;
@@ -107,6 +108,7 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
     }
     mat4_wide(gl, sl);
     mat4_wide(gh, sh);
+    uint64_t w[16];  // lanes whose output still needs + eps (one shared rare branch)
 #pragma unroll
     for (int j = 0; j < 16; j += 4) {
         uint64_t yl[4], yh[4];
@@ -120,20 +122,47 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
                 A = acc32s(A, (uint32_t)rc[j + k]);
                 B = acc32s(B, (uint32_t)(rc[j + k] >> 32));
             }
-            st[j + k] = gl_from_halves(A, B);
+            st[j + k] = gl_from_halves_defer(A, B, w[j + k]);
         }
+    }
+    uint64_t any = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) any |= w[i];
+    if (__builtin_expect(any != 0, 0)) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) gl_fold_eps(st[i], w[i]);
     }
 }
 
 // One internal round: st0 <- (st0 + rc)^7, then st_i <- sum + V_i st_i.
 // The round sum is formed from 32-bit halves (two 64-bit running sums, one
-// v_mad_u64_u32 per half) and made canonical, so that the lanes can use
-// single-correction forms:
-//   V = -2^-k (k = 3, 4, 5): x 2^-k = q - m eps with q = x >> k,
-//     m = (x mod 2^k) 2^(32-k), so sum - x 2^-k = (sum + m eps) - q;
-//   V = 2^-32: sum + x 2^-32 = (sum + x.hi) - x.lo eps, where sum + x.hi
-//     cannot wrap (sum <= p - 1) and x.lo eps < p;
-//   the other negative lanes subtract with gl_sub2.
+// v_mad_u64_u32 per half) and made canonical, sum = s0 + s1 2^32. Lanes then
+// use the cheapest of two kinds of form:
+//  * exact sums of halves A + B 2^32 (A, B below 2^35), reduced once with the
+//    final fold deferred to one shared rare branch:
+//      V = 2, 3, 4:  A = s0 + V x.lo, B = s1 + V x.hi;
+//      V = -3:       -3 x = 3 ~x - 3 (eps - 1) with ~x = 2^64 - 1 - x, and
+//                    -3 (eps - 1) = (2^32 - 4) 2^32 + 7 mod p, so
+//                    A = s0 + 7 + 3 ~x.lo, B = s1 + 2^32 - 4 + 3 ~x.hi;
+//      V = 2^-k (k = 3, 4, 5): x 2^-k = q - m eps with q = x >> k and
+//                    m = (x mod 2^k) 2^(32-k), and -m 2^32 = ~m 2^32 + 1
+//                    (2^32 eps = -1), so A = s0 + q.lo + m + 1,
+//                    B = s1 + q.hi + ~m (~m = 2^32 - 1 - m);
+//  * single-correction forms on the canonical sum:
+//      V = -2^-k: sum - x 2^-k = (sum + m eps) - q;
+//      V = 2^-32: sum + x 2^-32 = (sum + x.hi) - x.lo eps, where sum + x.hi
+//                 cannot wrap (sum <= p - 1) and x.lo eps < p;
+//      V = 1, 1/2: sum + t with one wrap correction; V = -2, -4, -1/2: gl_sub2.
+template <int K>
+__host__ __device__ __forceinline__ uint64_t lane_inv_pow2(uint64_t SL1, uint64_t SH, uint64_t x, uint64_t& w)
+{
+    const uint32_t ql = (uint32_t)(x >> K), qh = (uint32_t)(x >> 32) >> K;
+    const uint32_t m = (uint32_t)x << (32 - K);
+    const uint64_t A = acc32(acc32(SL1, ql), m);
+    const uint64_t B = acc32(acc32(SH, qh), ~m);
+    return gl_from_halves_defer(A, B, w);
+}
+
 template <bool DIAG15_IS_INV_2_32>
 __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t rc, uint64_t diag15)
 {
@@ -150,27 +179,47 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
     const uint64_t t = slo + (shi << 32);
     const uint32_t k = (uint32_t)(shi >> 32) + (t < slo ? 1u : 0u);
     const uint64_t sum = gl_canon_fast(gl_add_meps_rare(t, k));
+    const uint64_t SL = (uint32_t)sum, SH = sum >> 32;  // the halves of the sum, zero-extended
 
     const uint64_t x15 = st[15];
-    st[0] = gl_sub2(sum, gl_shl<1>(x0));                                   // -2
-    st[1] = gl_add_small(st[1], sum);                                      //  1
-    st[2] = gl_add_shl<1>(sum, st[2]);                                     //  2
-    st[3] = gl_add_small(gl_halve(st[3]), sum);                            //  1/2
-    st[4] = gl_add_small(gl_add_shl<1>(st[4], st[4]), sum);                //  3
-    st[5] = gl_add_shl<2>(sum, st[5]);                                     //  4
-    st[6] = gl_sub2(sum, gl_halve(st[6]));                                 // -1/2
-    st[7] = gl_sub2(sum, gl_add_shl<1>(st[7], st[7]));                     // -3
-    st[8] = gl_sub2(sum, gl_shl<2>(st[8]));                                // -4
-    st[9] = gl_add_small(gl_mul_inv_pow2<3>(st[9]), sum);                  //  1/2^3
-    st[10] = gl_add_small(gl_mul_inv_pow2<4>(st[10]), sum);                //  1/2^4
-    st[11] = gl_add_small(gl_mul_inv_pow2<5>(st[11]), sum);                //  1/2^5
-    st[12] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[12] << 29), st[12] >> 3);  // -1/2^3
-    st[13] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[13] << 28), st[13] >> 4);  // -1/2^4
-    st[14] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[14] << 27), st[14] >> 5);  // -1/2^5
+    uint64_t w[7];
+    st[0] = gl_sub2(sum, gl_shl<1>(x0));                                                      // -2
+    st[1] = gl_add_small(st[1], sum);                                                         //  1
+    st[2] = gl_from_halves_defer(acc32m<2>(SL, (uint32_t)st[2]), acc32m<2>(SH, (uint32_t)(st[2] >> 32)),
+                                 w[0]);                                                       //  2
+    st[3] = gl_add_small(gl_halve(st[3]), sum);                                               //  1/2
+    st[4] = gl_from_halves_defer(acc32m<3>(SL, (uint32_t)st[4]), acc32m<3>(SH, (uint32_t)(st[4] >> 32)),
+                                 w[1]);                                                       //  3
+    st[5] = gl_from_halves_defer(acc32m<4>(SL, (uint32_t)st[5]), acc32m<4>(SH, (uint32_t)(st[5] >> 32)),
+                                 w[2]);                                                       //  4
+    st[6] = gl_sub2(sum, gl_halve(st[6]));                                                    // -1/2
+    {
+        const uint64_t nx = ~st[7];                                                           // -3
+        st[7] = gl_from_halves_defer(acc32m<3>(SL + 7, (uint32_t)nx),
+                                     acc32m<3>(SH + 0xFFFFFFFCull, (uint32_t)(nx >> 32)), w[3]);
+    }
+    st[8] = gl_sub2(sum, gl_shl<2>(st[8]));                                                   // -4
+    const uint64_t SL1 = SL + 1;
+    st[9] = lane_inv_pow2<3>(SL1, SH, st[9], w[4]);                                           //  1/2^3
+    st[10] = lane_inv_pow2<4>(SL1, SH, st[10], w[5]);                                         //  1/2^4
+    st[11] = lane_inv_pow2<5>(SL1, SH, st[11], w[6]);                                         //  1/2^5
+    st[12] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[12] << 29), st[12] >> 3);            // -1/2^3
+    st[13] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[13] << 28), st[13] >> 4);            // -1/2^4
+    st[14] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[14] << 27), st[14] >> 5);            // -1/2^5
     if (DIAG15_IS_INV_2_32)
         st[15] = gl_sub_small(acc32(sum, (uint32_t)(x15 >> 32)), (uint64_t)(uint32_t)x15 * EPS);
     else
         st[15] = gl_add_small(gl_mul(x15, diag15), sum);
+    const uint64_t any = w[0] | w[1] | w[2] | w[3] | w[4] | w[5] | w[6];
+    if (__builtin_expect(any != 0, 0)) {
+        gl_fold_eps(st[2], w[0]);
+        gl_fold_eps(st[4], w[1]);
+        gl_fold_eps(st[5], w[2]);
+        gl_fold_eps(st[7], w[3]);
+        gl_fold_eps(st[9], w[4]);
+        gl_fold_eps(st[10], w[5]);
+        gl_fold_eps(st[11], w[6]);
+    }
 }
 
 template <bool DIAG15_IS_INV_2_32>
