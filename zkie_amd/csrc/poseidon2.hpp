@@ -141,9 +141,9 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
 //  * exact sums of halves A + B 2^32 (A, B below 2^35), reduced once with the
 //    final fold deferred to one shared rare branch:
 //      V = 2, 3, 4:  A = s0 + V x.lo, B = s1 + V x.hi;
-//      V = -3:       -3 x = 3 ~x - 3 (eps - 1) with ~x = 2^64 - 1 - x, and
-//                    -3 (eps - 1) = (2^32 - 4) 2^32 + 7 mod p, so
-//                    A = s0 + 7 + 3 ~x.lo, B = s1 + 2^32 - 4 + 3 ~x.hi;
+//      V = -v (v = 2, 3, 4): -v x = v ~x - v (eps - 1) with ~x = 2^64 - 1 - x,
+//                    and -v (eps - 1) = (2^32 - 1 - v) 2^32 + 1 + 2v mod p, so
+//                    A = s0 + 1 + 2v + v ~x.lo, B = s1 + 2^32 - 1 - v + v ~x.hi;
 //      V = 2^-k (k = 3, 4, 5): x 2^-k = q - m eps with q = x >> k and
 //                    m = (x mod 2^k) 2^(32-k), and -m 2^32 = ~m 2^32 + 1
 //                    (2^32 eps = -1), so A = s0 + q.lo + m + 1,
@@ -152,7 +152,7 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
 //      V = -2^-k: sum - x 2^-k = (sum + m eps) - q;
 //      V = 2^-32: sum + x 2^-32 = (sum + x.hi) - x.lo eps, where sum + x.hi
 //                 cannot wrap (sum <= p - 1) and x.lo eps < p;
-//      V = 1, 1/2: sum + t with one wrap correction; V = -2, -4, -1/2: gl_sub2.
+//      V = 1, 1/2: sum + t with one wrap correction; V = -1/2: gl_sub2.
 template <int K>
 __host__ __device__ __forceinline__ uint64_t lane_inv_pow2(uint64_t SL1, uint64_t SH, uint64_t x, uint64_t& w)
 {
@@ -182,8 +182,12 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
     const uint64_t SL = (uint32_t)sum, SH = sum >> 32;  // the halves of the sum, zero-extended
 
     const uint64_t x15 = st[15];
-    uint64_t w[7];
-    st[0] = gl_sub2(sum, gl_shl<1>(x0));                                                      // -2
+    uint64_t w[9];
+    {
+        const uint64_t nx = ~x0;                                                              // -2
+        st[0] = gl_from_halves_defer(acc32m<2>(SL + 5, (uint32_t)nx),
+                                     acc32m<2>(SH + 0xFFFFFFFDull, (uint32_t)(nx >> 32)), w[7]);
+    }
     st[1] = gl_add_small(st[1], sum);                                                         //  1
     st[2] = gl_from_halves_defer(acc32m<2>(SL, (uint32_t)st[2]), acc32m<2>(SH, (uint32_t)(st[2] >> 32)),
                                  w[0]);                                                       //  2
@@ -198,7 +202,11 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
         st[7] = gl_from_halves_defer(acc32m<3>(SL + 7, (uint32_t)nx),
                                      acc32m<3>(SH + 0xFFFFFFFCull, (uint32_t)(nx >> 32)), w[3]);
     }
-    st[8] = gl_sub2(sum, gl_shl<2>(st[8]));                                                   // -4
+    {
+        const uint64_t nx = ~st[8];                                                           // -4
+        st[8] = gl_from_halves_defer(acc32m<4>(SL + 9, (uint32_t)nx),
+                                     acc32m<4>(SH + 0xFFFFFFFBull, (uint32_t)(nx >> 32)), w[8]);
+    }
     const uint64_t SL1 = SL + 1;
     st[9] = lane_inv_pow2<3>(SL1, SH, st[9], w[4]);                                           //  1/2^3
     st[10] = lane_inv_pow2<4>(SL1, SH, st[10], w[5]);                                         //  1/2^4
@@ -210,8 +218,10 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
         st[15] = gl_sub_small(acc32(sum, (uint32_t)(x15 >> 32)), (uint64_t)(uint32_t)x15 * EPS);
     else
         st[15] = gl_add_small(gl_mul(x15, diag15), sum);
-    const uint64_t any = w[0] | w[1] | w[2] | w[3] | w[4] | w[5] | w[6];
+    const uint64_t any = w[0] | w[1] | w[2] | w[3] | w[4] | w[5] | w[6] | w[7] | w[8];
     if (__builtin_expect(any != 0, 0)) {
+        gl_fold_eps(st[0], w[7]);
+        gl_fold_eps(st[8], w[8]);
         gl_fold_eps(st[2], w[0]);
         gl_fold_eps(st[4], w[1]);
         gl_fold_eps(st[5], w[2]);
