@@ -37,6 +37,7 @@ void run_pass_t(const PassArgs& a, uint32_t T)
             for (uint32_t tid = 0; tid < T; tid++)
                 pass_step0_gather<S, KNZ, LOGV>(a, t, pass_lane(a, t, tid), tid, T, x[tid]);
         for (uint32_t tid = 0; tid < T; tid++) pass_tables<S, ROLE>(a, t, tid, T, lds.data());
+        for (uint32_t tid = 0; tid < T; tid++) pass_tables_tab<S, ROLE>(t, tid, T, lds.data());
         for (int k = 0; k < n; k++)
             for (uint32_t tid = 0; tid < T; tid++) {
                 const PassLane l = pass_lane(a, t, tid);

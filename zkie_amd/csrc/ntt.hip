@@ -62,10 +62,12 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
     } else {
         static_assert(((1u << (S - Radix<S>::r0)) << 4) <= kStepU * T, "step 0 in one round");
         // The tile's HBM reads go out first; the twiddle tables are filled in
-        // LDS while they are in flight, so the two latencies overlap.
+        // LDS while they are in flight, so the latencies overlap.
         uint64_t x[kStepU][1 << Radix<S>::r0];
         pass_step0_gather<S, KNZ, LOGV>(a, t, l, tid, T, x);
         pass_tables<S, ROLE>(a, t, tid, T, lds);
+        __syncthreads();
+        pass_tables_tab<S, ROLE>(t, tid, T, lds);
         __syncthreads();  // step twiddles in LDS before step 0 reads them
         pass_step0_finish<S, INV, ROLE, LOGV>(a, t, l, tid, T, lds, x);
         __syncthreads();

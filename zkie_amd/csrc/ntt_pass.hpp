@@ -431,7 +431,8 @@ __host__ __device__ __forceinline__ bool pass_uses_twtab(const PassArgs& a)
 }
 
 // LDS words of a multi-step pass: the 2^S x V tile, the inter-pass twiddle
-// table (kRoleTable), then the step twiddles w_512^k (kW512Words).
+// table (kRoleTable), then the step twiddles w_512^k (kW512Words), then
+// (kRoleTable) the two small power tables the inter-pass table is formed from.
 constexpr uint32_t kW512Words = 1u << kStepTableLg;
 template <int S, int ROLE>
 __host__ __device__ __forceinline__ uint32_t pass_wtab_offset(uint32_t logV)
@@ -439,28 +440,51 @@ __host__ __device__ __forceinline__ uint32_t pass_wtab_offset(uint32_t logV)
     return ((1u << S) << logV) + (ROLE == kRoleTable ? (1u << S) : 0u);
 }
 
-// Before step 0 (a barrier separates this from step 0, the first reader):
-// the step twiddles w_512^k into LDS and, for kRoleTable, the tile's
-// inter-pass twiddles w_N^(i1 j2) (read by the last step), in one loop so
-// that the global reads of both tables are in flight together.
+// The inter-pass table of a kRoleTable tile, tab[i] = w_N^(i j2) for
+// i < 2^S, is formed as lo[i mod 32] hi[i / 32] from two small power tables
+// (lo[k] = w_N^(k j2), hi[m] = w_N^(32 m j2)), so a workgroup reads 2 (32 +
+// 2^(S-5)) entries of the two-level root table instead of 2^(S+1), which
+// the streaming codeword would evict from L2 between workgroups. The small
+// tables sit in LDS after the step twiddles.
+constexpr uint32_t kTabLoLg = 5;
+template <int S>
+__host__ __device__ __forceinline__ constexpr uint32_t pass_tab_lo_lg()
+{
+    return S < (int)kTabLoLg ? (uint32_t)S : kTabLoLg;
+}
+
+// Before step 0, first half (a barrier follows): the step twiddles w_512^k
+// into LDS and, for kRoleTable, the two small power tables.
 template <int S, int ROLE>
 __host__ __device__ __forceinline__ void pass_tables(const PassArgs& a, const PassTile& t, uint32_t tid,
                                                      uint32_t T, uint64_t* lds)
 {
     if (S <= 3) return;
     uint64_t* wtab = lds + pass_wtab_offset<S, ROLE>(t.logV);
-    uint64_t* tab = lds + ((1u << S) << t.logV);
-    constexpr uint32_t len = kW512Words > (1u << S) ? kW512Words : (1u << S);
-    for (uint32_t i = tid; i < len; i += T) {
-        const uint64_t w = i < kW512Words ? a.w512[i] : 0;
-        uint64_t tw = 1;
-        if (ROLE == kRoleTable && i < (1u << S)) {
-            const uint64_t ex = (uint64_t)i * t.j20;
-            if (ex) tw = pass_root_pow(a, ex);
+    for (uint32_t i = tid; i < kW512Words; i += T) wtab[i] = a.w512[i];
+    if (ROLE == kRoleTable) {
+        constexpr uint32_t LO = pass_tab_lo_lg<S>();
+        constexpr uint32_t nlo = 1u << LO, nhi = 1u << (S - LO);
+        uint64_t* small = wtab + kW512Words;  // [lo | hi]
+        for (uint32_t i = tid; i < nlo + nhi; i += T) {
+            const uint64_t ex = (i < nlo ? (uint64_t)i : (uint64_t)(i - nlo) << LO) * t.j20;
+            small[i] = ex ? pass_root_pow(a, ex) : 1;
         }
-        if (i < kW512Words) wtab[i] = w;
-        if (ROLE == kRoleTable && i < (1u << S)) tab[i] = tw;
     }
+}
+
+// Before step 0, second half (after a barrier; a barrier separates it from
+// the last step, the reader): tab[i] = lo[i mod 2^LO] hi[i >> LO].
+template <int S, int ROLE>
+__host__ __device__ __forceinline__ void pass_tables_tab(const PassTile& t, uint32_t tid, uint32_t T,
+                                                         uint64_t* lds)
+{
+    if (ROLE != kRoleTable || S <= 3) return;
+    constexpr uint32_t LO = pass_tab_lo_lg<S>();
+    const uint64_t* small = lds + pass_wtab_offset<S, ROLE>(t.logV) + kW512Words;
+    uint64_t* tab = lds + ((1u << S) << t.logV);
+    for (uint32_t i = tid; i < (1u << S); i += T)
+        tab[i] = gl_mul(small[i & ((1u << LO) - 1)], small[(1u << LO) + (i >> LO)]);
 }
 
 // Step `k` of the S-point sub-DFT (k < pass_steps<S>()). The caller puts a

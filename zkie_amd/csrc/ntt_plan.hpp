@@ -153,7 +153,10 @@ inline size_t pass_lds_bytes(const PassArgs& a)
 {
     if (a.s <= 3) return 0;
     size_t words = (size_t)1 << (a.s + a.logC + a.logJ);
-    if (pass_uses_twtab(a)) words += (size_t)1 << a.s;
+    if (pass_uses_twtab(a)) {
+        const uint32_t lo = a.s < kTabLoLg ? a.s : kTabLoLg;
+        words += ((size_t)1 << a.s) + ((size_t)1 << lo) + ((size_t)1 << (a.s - lo));
+    }
     words += kW512Words;
     return words * 8;
 }
