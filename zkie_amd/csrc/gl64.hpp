@@ -416,6 +416,20 @@ __host__ __device__ __forceinline__ uint64_t gl_from_halves_defer(uint64_t A, ui
 #endif
 }
 
+// a | b of two lane masks held in scalar registers, formed on the scalar
+// unit (several deferred-fold masks are merged so that one branch serves
+// them all).
+__host__ __device__ __forceinline__ uint64_t mask_or(uint64_t a, uint64_t b)
+{
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    uint64_t r;
+    asm("s_or_b64 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b) : "scc");
+    return r;
+#else
+    return a | b;
+#endif
+}
+
 // r += eps in the lanes of mask w (a product-add of at most 2^32 eps wrapped
 // there, so the value is below 2^64 - 2^33 and + eps cannot wrap again).
 __host__ __device__ __forceinline__ void gl_fold_eps(uint64_t& r, uint64_t w)

@@ -218,7 +218,8 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
         st[15] = gl_sub_small(acc32(sum, (uint32_t)(x15 >> 32)), (uint64_t)(uint32_t)x15 * EPS);
     else
         st[15] = gl_add_small(gl_mul(x15, diag15), sum);
-    const uint64_t any = w[0] | w[1] | w[2] | w[3] | w[4] | w[5] | w[6] | w[7] | w[8];
+    const uint64_t any = mask_or(mask_or(mask_or(w[0], w[1]), mask_or(w[2], w[3])),
+                                 mask_or(mask_or(w[4], w[5]), mask_or(mask_or(w[6], w[7]), w[8])));
     if (__builtin_expect(any != 0, 0)) {
         gl_fold_eps(st[0], w[7]);
         gl_fold_eps(st[8], w[8]);
