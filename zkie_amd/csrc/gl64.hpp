@@ -371,20 +371,14 @@ __host__ __device__ __forceinline__ uint64_t acc32s(uint64_t acc, uint32_t x)
 }
 
 // A + B 2^32 mod p for A, B < 2^63 (sums of 32-bit halves): with
-// t = A + (B.lo << 32) and its carry c, the value is t + (B.hi + c) 2^64
-// and 2^64 = eps. For the sums of a linear layer B.hi + c is a small count,
-// so the final fold is a rare correction.
+// Bp = B + A.hi (one v_mad_u64_u32) the value is A.lo + Bp.lo 2^32 +
+// Bp.hi 2^64, and 2^64 = eps. For the sums of a linear layer Bp.hi is a
+// small count, so the final fold is a rare correction.
 __host__ __device__ __forceinline__ uint64_t gl_from_halves(uint64_t A, uint64_t B)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
-    uint32_t th, k;
-    uint64_t m;
-    asm("v_add_co_u32_e64 %0, %2, %3, %4\n\t"
-        "s_nop 1\n\t"
-        "v_addc_co_u32_e64 %1, %2, %5, 0, %2"
-        : "=&v"(th), "=&v"(k), "=&s"(m)
-        : "v"((uint32_t)(A >> 32)), "v"((uint32_t)B), "v"((uint32_t)(B >> 32)));
-    return gl_add_meps_rare(((uint64_t)th << 32) | (uint32_t)A, k);
+    const uint64_t Bp = acc32(B, (uint32_t)(A >> 32));
+    return gl_add_meps_rare(((uint64_t)(uint32_t)Bp << 32) | (uint32_t)A, (uint32_t)(Bp >> 32));
 #else
     const uint64_t t = A + (B << 32);
     const uint32_t k = (uint32_t)(B >> 32) + (t < A ? 1u : 0u);
@@ -399,16 +393,11 @@ __host__ __device__ __forceinline__ uint64_t gl_from_halves(uint64_t A, uint64_t
 __host__ __device__ __forceinline__ uint64_t gl_from_halves_defer(uint64_t A, uint64_t B, uint64_t& w)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
-    uint32_t th, k;
-    uint64_t m, S;
-    asm("v_add_co_u32_e64 %0, %2, %3, %4\n\t"
-        "s_nop 1\n\t"
-        "v_addc_co_u32_e64 %1, %2, %5, 0, %2"
-        : "=&v"(th), "=&v"(k), "=&s"(m)
-        : "v"((uint32_t)(A >> 32)), "v"((uint32_t)B), "v"((uint32_t)(B >> 32)));
+    const uint64_t Bp = acc32(B, (uint32_t)(A >> 32));
+    uint64_t S;
     asm("v_mad_u64_u32 %0, %1, %2, -1, %3"
         : "=&v"(S), "=s"(w)
-        : "v"(k), "v"(((uint64_t)th << 32) | (uint32_t)A));
+        : "v"((uint32_t)(Bp >> 32)), "v"(((uint64_t)(uint32_t)Bp << 32) | (uint32_t)A));
     return S;
 #else
     w = 0;
