@@ -26,6 +26,12 @@ constexpr uint64_t INV_2_32 = 0xFFFFFFFE00000002ull;  // 2^-32 mod p
 
 __host__ __device__ __forceinline__ uint64_t gl_canon(uint64_t a) { return a >= P ? a - P : a; }
 
+// Device forms written with gfx950 carry/borrow masks in inline assembly
+// (1); 0 builds the portable C forms on the device as well.
+#ifndef ZK_MUL_ASM
+#define ZK_MUL_ASM 1
+#endif
+
 // Rare corrections. Several reductions end in a correction that a lane needs
 // with probability about 2^-32 or less (a second wrap or borrow that only
 // operands near 2^64 can cause). On the device such a correction runs behind
@@ -43,15 +49,35 @@ __host__ __device__ __forceinline__ bool any_lane(bool c)
 }
 #define ZK_RARE(c) __builtin_expect(any_lane(c), 0)
 
+__host__ __device__ __forceinline__ void gl_fold_eps(uint64_t& r, uint64_t w);
+
 // a + b for any a, b < 2^64.
 __host__ __device__ __forceinline__ uint64_t gl_add(uint64_t a, uint64_t b)
 {
+#if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    // The carry of the 64-bit add (v_addc's carry-out) selects + eps, added
+    // by a product-add whose own carry-out marks the rare second wrap.
+    uint32_t s0, s1, c;
+    uint64_t k, w;
+    asm("v_add_co_u32_e64 %0, %3, %4, %5\n\t"
+        "s_nop 1\n\t"
+        "v_addc_co_u32_e64 %1, %3, %6, %7, %3\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32_e64 %2, 0, 1, %3"
+        : "=&v"(s0), "=&v"(s1), "=&v"(c), "=&s"(k)
+        : "v"((uint32_t)a), "v"((uint32_t)b), "v"((uint32_t)(a >> 32)), "v"((uint32_t)(b >> 32)));
+    uint64_t t;
+    asm("v_mad_u64_u32 %0, %1, %2, -1, %3" : "=&v"(t), "=s"(w) : "v"(c), "v"(((uint64_t)s1 << 32) | s0));
+    if (__builtin_expect(w != 0, 0)) gl_fold_eps(t, w);
+    return t;
+#else
     uint64_t s = a + b;
     uint64_t t = s + ((s < a) ? EPS : 0);
     // A second wrap needs both operands at least p: rare, folded the same way.
     const bool w2 = t < s;
     if (ZK_RARE(w2)) t += w2 ? EPS : 0;
     return t;
+#endif
 }
 
 // a + b where b < p (or any b <= 2^64 - 2^32): a single wrap at most.
@@ -90,12 +116,8 @@ __host__ __device__ __forceinline__ uint64_t gl_reduce128(uint64_t lo, uint64_t 
     return r;
 }
 
-#ifndef ZK_MUL_ASM
-#define ZK_MUL_ASM 1
-#endif
-
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
-// a * b mod p in 15 VALU instructions on gfx950, using the carry-out of
+// a * b mod p in 12 VALU instructions on gfx950, using the carry-out of
 // v_mad_u64_u32, which the compiler does not use on its own:
 //   P = a0 b0,  T = a0 b1 + P.hi,  U + c 2^64 = a1 b0 + T  (carry c kept as a lane mask),
 //   H = a1 b1 + U.hi,  L = U.lo 2^32 + P.lo,
@@ -453,7 +475,14 @@ __host__ __device__ __forceinline__ uint64_t gl_mul_inv_pow2(uint64_t x)
 // x * 2^24: x << 24 plus the shifted-out bits hi < 2^24 at weight 2^64 = eps.
 __host__ __device__ __forceinline__ uint64_t gl_mul_2e24(uint64_t x)
 {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // x << 24 from the halves directly: (lo << 24, hi:lo >> 8)
+    const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+    const uint64_t s = ((uint64_t)__builtin_amdgcn_alignbit(hi, lo, 8) << 32) | (uint32_t)(lo << 24);
+    return gl_add_meps(s, hi >> 8);
+#else
     return gl_add_meps(x << 24, (uint32_t)(x >> 40));
+#endif
 }
 
 // x * 2^48: hi = x >> 16 (48 bits) at weight 2^64; hi eps = hi.lo eps + hi.hi 2^32 eps
