@@ -42,7 +42,7 @@ void run_pass_t(const PassArgs& a, uint32_t T)
             for (uint32_t tid = 0; tid < T; tid++) {
                 const PassLane l = pass_lane(a, t, tid);
                 if (k == 0 && split0) {
-                    if constexpr (n > 1) pass_step0_finish<S, INV, ROLE, LOGV>(a, t, l, tid, T, lds.data(), x[tid]);
+                    if constexpr (n > 1) pass_step0_finish<S, KNZ, INV, ROLE, LOGV>(a, t, l, tid, T, lds.data(), x[tid]);
                 } else {
                     pass_step<S, KNZ, INV, ROLE, LOGV>(k, a, t, l, tid, T, lds.data());
                 }

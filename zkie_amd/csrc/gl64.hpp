@@ -49,6 +49,11 @@ __host__ __device__ __forceinline__ bool any_lane(bool c)
 }
 #define ZK_RARE(c) __builtin_expect(any_lane(c), 0)
 
+// An operand the compiler has proven to be 0 after inlining (e.g. the
+// zero-padded inputs of a DFT): the assembly forms below, which the compiler
+// cannot fold, return early for it.
+#define ZK_ZERO(x) (__builtin_constant_p(x) && (x) == 0)
+
 __host__ __device__ __forceinline__ void gl_fold_eps(uint64_t& r, uint64_t w);
 
 // a + b for any a, b < 2^64.
@@ -57,6 +62,8 @@ __host__ __device__ __forceinline__ uint64_t gl_add(uint64_t a, uint64_t b)
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
     // The carry of the 64-bit add (v_addc's carry-out) selects + eps, added
     // by a product-add whose own carry-out marks the rare second wrap.
+    if (ZK_ZERO(b)) return a;
+    if (ZK_ZERO(a)) return b;
     uint32_t s0, s1, c;
     uint64_t k, w;
     asm("v_add_co_u32_e64 %0, %3, %4, %5\n\t"
@@ -268,6 +275,7 @@ __host__ __device__ __forceinline__ void gl_mul2(uint64_t a, uint64_t b, uint64_
 __host__ __device__ __forceinline__ uint64_t gl_sub_small(uint64_t a, uint64_t b)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    if (ZK_ZERO(b)) return a;
     uint32_t d0, d1, e;
     uint64_t k;
     asm("v_sub_co_u32_e64 %0, %3, %4, %6\n\t"
@@ -293,6 +301,7 @@ __host__ __device__ __forceinline__ uint64_t gl_sub_small(uint64_t a, uint64_t b
 __host__ __device__ __forceinline__ uint64_t gl_sub2(uint64_t a, uint64_t b)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    if (ZK_ZERO(b)) return a;
     uint32_t d0, d1, e;
     uint64_t k;
     asm("v_sub_co_u32_e64 %0, %3, %4, %6\n\t"
@@ -317,6 +326,7 @@ __host__ __device__ __forceinline__ uint64_t gl_sub2(uint64_t a, uint64_t b)
 __host__ __device__ __forceinline__ uint64_t gl_add_meps(uint64_t s, uint32_t m)
 {
 #if defined(__HIP_DEVICE_COMPILE__) && ZK_MUL_ASM
+    if (ZK_ZERO(m)) return s;
     uint64_t S, k;
     uint32_t c;
     asm("v_mad_u64_u32 %0, %1, %3, -1, %4\n\t"
@@ -466,6 +476,7 @@ template <int K>
 __host__ __device__ __forceinline__ uint64_t gl_mul_inv_pow2(uint64_t x)
 {
     static_assert(K >= 1 && K <= 32, "shift range");
+    if (ZK_ZERO(x)) return 0;
     const uint64_t q = x >> K;
     const uint64_t m = (K == 32) ? (x & 0xFFFFFFFFull) : ((x & ((1ull << K) - 1)) << (32 - K));
     const uint64_t y = ((0xFFFFFFFFull - m) << 32) + (m + 1);
@@ -475,6 +486,7 @@ __host__ __device__ __forceinline__ uint64_t gl_mul_inv_pow2(uint64_t x)
 // x * 2^24: x << 24 plus the shifted-out bits hi < 2^24 at weight 2^64 = eps.
 __host__ __device__ __forceinline__ uint64_t gl_mul_2e24(uint64_t x)
 {
+    if (ZK_ZERO(x)) return 0;
 #if defined(__HIP_DEVICE_COMPILE__)
     // x << 24 from the halves directly: (lo << 24, hi:lo >> 8)
     const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
@@ -489,6 +501,7 @@ __host__ __device__ __forceinline__ uint64_t gl_mul_2e24(uint64_t x)
 // and 2^32 eps = 2^64 - 2^32 = -1, so x 2^48 = (x << 48) + hi.lo eps - hi.hi.
 __host__ __device__ __forceinline__ uint64_t gl_mul_2e48(uint64_t x)
 {
+    if (ZK_ZERO(x)) return 0;
     const uint64_t hi = x >> 16;
     return gl_sub_small(gl_add_meps(x << 48, (uint32_t)hi), hi >> 32);
 }

@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
         __syncthreads();
         pass_tables_tab<S, ROLE>(t, tid, T, lds);
         __syncthreads();  // step twiddles in LDS before step 0 reads them
-        pass_step0_finish<S, INV, ROLE, LOGV>(a, t, l, tid, T, lds, x);
+        pass_step0_finish<S, KNZ, INV, ROLE, LOGV>(a, t, l, tid, T, lds, x);
         __syncthreads();
         pass_step<S, KNZ, INV, ROLE, LOGV>(1, a, t, l, tid, T, lds);
     }

@@ -185,51 +185,41 @@ __host__ __device__ __forceinline__ uint64_t dif_lower8(uint64_t u, uint64_t v)
 }
 
 // In-register R-point DFT (radix-2 DIF); x[idx] ends up holding frequency
-// bit_reverse(idx, log2 R).
-template <int RLOG, bool INV>
+// bit_reverse(idx, log2 R). Inputs x[k] with k >= NZ are known to be zero
+// (the zero padding of an LDE): they enter as literal zeros, so that the
+// butterflies they reach fold away at compile time.
+template <int RLOG, bool INV, int NZ = (1 << RLOG)>
 __host__ __device__ __forceinline__ void dft_small(uint64_t* x)
 {
     if (RLOG == 3) {
-        {
-            const uint64_t u0 = x[0], v0 = x[4], u1 = x[1], v1 = x[5];
-            const uint64_t u2 = x[2], v2 = x[6], u3 = x[3], v3 = x[7];
-            x[0] = gl_add(u0, v0);
-            x[1] = gl_add(u1, v1);
-            x[2] = gl_add(u2, v2);
-            x[3] = gl_add(u3, v3);
-            x[4] = dif_lower8<INV, 0>(u0, v0);
-            x[5] = dif_lower8<INV, 1>(u1, v1);
-            x[6] = dif_lower8<INV, 2>(u2, v2);
-            x[7] = dif_lower8<INV, 3>(u3, v3);
-        }
-#pragma unroll
-        for (int h = 0; h < 8; h += 4) {
-            const uint64_t u0 = x[h], v0 = x[h + 2], u1 = x[h + 1], v1 = x[h + 3];
-            x[h] = gl_add(u0, v0);
-            x[h + 1] = gl_add(u1, v1);
-            x[h + 2] = dif_lower8<INV, 0>(u0, v0);
-            x[h + 3] = dif_lower8<INV, 2>(u1, v1);  // w4 = w8^2
-        }
-#pragma unroll
-        for (int q = 0; q < 8; q += 2) {
-            const uint64_t u = x[q], v = x[q + 1];
-            x[q] = gl_add(u, v);
-            x[q + 1] = gl_sub2(u, v);
-        }
+        const uint64_t a0 = x[0], a1 = NZ > 1 ? x[1] : 0, a2 = NZ > 2 ? x[2] : 0, a3 = NZ > 3 ? x[3] : 0;
+        const uint64_t a4 = NZ > 4 ? x[4] : 0, a5 = NZ > 5 ? x[5] : 0, a6 = NZ > 6 ? x[6] : 0,
+                       a7 = NZ > 7 ? x[7] : 0;
+        const uint64_t b0 = gl_add(a0, a4), b1 = gl_add(a1, a5), b2 = gl_add(a2, a6), b3 = gl_add(a3, a7);
+        const uint64_t b4 = dif_lower8<INV, 0>(a0, a4), b5 = dif_lower8<INV, 1>(a1, a5);
+        const uint64_t b6 = dif_lower8<INV, 2>(a2, a6), b7 = dif_lower8<INV, 3>(a3, a7);
+        const uint64_t c0 = gl_add(b0, b2), c1 = gl_add(b1, b3);
+        const uint64_t c2 = dif_lower8<INV, 0>(b0, b2), c3 = dif_lower8<INV, 2>(b1, b3);  // w4 = w8^2
+        const uint64_t c4 = gl_add(b4, b6), c5 = gl_add(b5, b7);
+        const uint64_t c6 = dif_lower8<INV, 0>(b4, b6), c7 = dif_lower8<INV, 2>(b5, b7);
+        x[0] = gl_add(c0, c1);
+        x[1] = gl_sub2(c0, c1);
+        x[2] = gl_add(c2, c3);
+        x[3] = gl_sub2(c2, c3);
+        x[4] = gl_add(c4, c5);
+        x[5] = gl_sub2(c4, c5);
+        x[6] = gl_add(c6, c7);
+        x[7] = gl_sub2(c6, c7);
     } else if (RLOG == 2) {
-        const uint64_t u0 = x[0], v0 = x[2], u1 = x[1], v1 = x[3];
-        x[0] = gl_add(u0, v0);
-        x[1] = gl_add(u1, v1);
-        x[2] = dif_lower8<INV, 0>(u0, v0);
-        x[3] = dif_lower8<INV, 2>(u1, v1);
-#pragma unroll
-        for (int q = 0; q < 4; q += 2) {
-            const uint64_t u = x[q], v = x[q + 1];
-            x[q] = gl_add(u, v);
-            x[q + 1] = gl_sub2(u, v);
-        }
+        const uint64_t a0 = x[0], a1 = NZ > 1 ? x[1] : 0, a2 = NZ > 2 ? x[2] : 0, a3 = NZ > 3 ? x[3] : 0;
+        const uint64_t b0 = gl_add(a0, a2), b1 = gl_add(a1, a3);
+        const uint64_t b2 = dif_lower8<INV, 0>(a0, a2), b3 = dif_lower8<INV, 2>(a1, a3);
+        x[0] = gl_add(b0, b1);
+        x[1] = gl_sub2(b0, b1);
+        x[2] = gl_add(b2, b3);
+        x[3] = gl_sub2(b2, b3);
     } else if (RLOG == 1) {
-        const uint64_t u = x[0], v = x[1];
+        const uint64_t u = x[0], v = NZ > 1 ? x[1] : 0;
         x[0] = gl_add(u, v);
         x[1] = gl_sub2(u, v);
     }
@@ -328,7 +318,7 @@ __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const Pa
 // w_{2^BS}^(f q) from the LDS table wtab (w_512^k), then the outputs to the
 // LDS tile or, in the last step (TO_GLOBAL), with the pass role's treatment
 // to HBM.
-template <int S, int RL, int BS, bool INV, bool TO_GLOBAL, int ROLE, int LOGV>
+template <int S, int RL, int BS, bool INV, bool TO_GLOBAL, int ROLE, int LOGV, int NZ = (1 << RL)>
 __host__ __device__ __forceinline__ void step_finish(const PassArgs& a, const PassTile& t, const PassLane& l,
                                                      uint32_t it0, uint32_t T, uint64_t* lds,
                                                      const uint64_t* wtab, const uint64_t* twtab,
@@ -355,7 +345,7 @@ __host__ __device__ __forceinline__ void step_finish(const PassArgs& a, const Pa
                 tw[idx] = wtab[wi];
             }
         }
-        dft_small<RL, INV>(x[u]);
+        dft_small<RL, INV, (NZ < (1 << RL) ? NZ : (1 << RL))>(x[u]);
         if (QL > 0) {
 #pragma unroll
             for (int idx = 1; idx < R; idx++) x[u][idx] = gl_mul(x[u][idx], tw[idx]);
@@ -409,7 +399,7 @@ __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassT
     for (uint32_t it0 = tid; it0 < items; it0 += kStepU * T) {
         uint64_t x[kStepU][1 << RL];
         step_gather<S, RL, BS, KNZ, FROM_GLOBAL, LOGV>(a, t, l, it0, T, lds, x);
-        step_finish<S, RL, BS, INV, TO_GLOBAL, ROLE, LOGV>(a, t, l, it0, T, lds, wtab, twtab, x);
+        step_finish<S, RL, BS, INV, TO_GLOBAL, ROLE, LOGV, FROM_GLOBAL ? KNZ : 8>(a, t, l, it0, T, lds, wtab, twtab, x);
     }
 }
 
@@ -524,7 +514,7 @@ __host__ __device__ __forceinline__ void pass_step0_gather(const PassArgs& a, co
     step_gather<S, Radix<S>::r0, S, KNZ, true, LOGV>(a, t, l, tid, T, nullptr, x);
 }
 
-template <int S, bool INV, int ROLE, int LOGV>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV>
 __host__ __device__ __forceinline__ void pass_step0_finish(const PassArgs& a, const PassTile& t,
                                                            const PassLane& l, uint32_t tid, uint32_t T,
                                                            uint64_t* lds,
@@ -532,7 +522,7 @@ __host__ __device__ __forceinline__ void pass_step0_finish(const PassArgs& a, co
 {
     static_assert(Radix<S>::n > 1, "a single-step pass writes HBM from step 0");
     const uint64_t* wtab = lds + pass_wtab_offset<S, ROLE>(t.logV);
-    step_finish<S, Radix<S>::r0, S, INV, false, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr, x);
+    step_finish<S, Radix<S>::r0, S, INV, false, ROLE, LOGV, KNZ>(a, t, l, tid, T, lds, wtab, nullptr, x);
 }
 
 // Role of a pass (see PassRole).
