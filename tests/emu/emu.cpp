@@ -53,8 +53,8 @@ void run_pass_t(const PassArgs& a, uint32_t T)
 template <int S, int KNZ, bool INV, int ROLE>
 void run_pass_v(const PassArgs& a, uint32_t T)
 {
-    if (a.logC + a.logJ == 4)
-        run_pass_t<S, KNZ, INV, ROLE, 4>(a, T);
+    if (a.logC + a.logJ == kNttLogV)
+        run_pass_t<S, KNZ, INV, ROLE, (int)kNttLogV>(a, T);
     else
         run_pass_t<S, KNZ, INV, ROLE, -1>(a, T);
 }

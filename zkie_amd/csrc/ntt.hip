@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
     if constexpr (n == 1) {
         pass_step<S, KNZ, INV, ROLE, LOGV>(0, a, t, l, tid, T, lds);
     } else {
-        static_assert(((1u << (S - Radix<S>::r0)) << 4) <= kStepU * T, "step 0 in one round");
+        static_assert(((1u << (S - Radix<S>::r0)) << kNttLogV) <= kStepU * T, "step 0 in one round");
         // The tile's HBM reads go out first; the twiddle tables are filled in
         // LDS while they are in flight, so the latencies overlap.
         uint64_t x[kStepU][1 << Radix<S>::r0];
@@ -108,7 +108,7 @@ hipError_t launch_one(const PassArgs& a, uint64_t blocks, size_t shmem, hipStrea
 template <int S, int KNZ, bool INV, int ROLE>
 hipError_t launch_v(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
 {
-    if (a.logC + a.logJ == 4) return launch_one<S, KNZ, INV, ROLE, 4>(a, blocks, shmem, s);
+    if (a.logC + a.logJ == kNttLogV) return launch_one<S, KNZ, INV, ROLE, (int)kNttLogV>(a, blocks, shmem, s);
     return launch_one<S, KNZ, INV, ROLE, -1>(a, blocks, shmem, s);
 }
 

@@ -421,8 +421,7 @@ __host__ __device__ __forceinline__ bool pass_uses_twtab(const PassArgs& a)
 }
 
 // LDS words of a multi-step pass: the 2^S x V tile, the inter-pass twiddle
-// table (kRoleTable), then the step twiddles w_512^k (kW512Words), then
-// (kRoleTable) the two small power tables the inter-pass table is formed from.
+// table (kRoleTable), then the step twiddles w_512^k (kW512Words).
 constexpr uint32_t kW512Words = 1u << kStepTableLg;
 template <int S, int ROLE>
 __host__ __device__ __forceinline__ uint32_t pass_wtab_offset(uint32_t logV)
@@ -435,12 +434,13 @@ __host__ __device__ __forceinline__ uint32_t pass_wtab_offset(uint32_t logV)
 // (lo[k] = w_N^(k j2), hi[m] = w_N^(32 m j2)), so a workgroup reads 2 (32 +
 // 2^(S-5)) entries of the two-level root table instead of 2^(S+1), which
 // the streaming codeword would evict from L2 between workgroups. The small
-// tables sit in LDS after the step twiddles.
+// tables sit at the start of the tile region, which step 0 writes only after
+// the inter-pass table is formed (a barrier separates the two).
 constexpr uint32_t kTabLoLg = 5;
 template <int S>
 __host__ __device__ __forceinline__ constexpr uint32_t pass_tab_lo_lg()
 {
-    return S < (int)kTabLoLg ? (uint32_t)S : kTabLoLg;
+    return S <= (int)kTabLoLg ? (uint32_t)S - 1 : kTabLoLg;
 }
 
 // Before step 0, first half (a barrier follows): the step twiddles w_512^k
@@ -455,7 +455,9 @@ __host__ __device__ __forceinline__ void pass_tables(const PassArgs& a, const Pa
     if (ROLE == kRoleTable) {
         constexpr uint32_t LO = pass_tab_lo_lg<S>();
         constexpr uint32_t nlo = 1u << LO, nhi = 1u << (S - LO);
-        uint64_t* small = wtab + kW512Words;  // [lo | hi]
+        uint64_t* small = lds;  // [lo | hi], in the tile region
+        static_assert(S <= 3 || (1u << pass_tab_lo_lg<S>()) + (1u << (S - pass_tab_lo_lg<S>())) <= (1u << S),
+                      "small tables fit the tile region");
         for (uint32_t i = tid; i < nlo + nhi; i += T) {
             const uint64_t ex = (i < nlo ? (uint64_t)i : (uint64_t)(i - nlo) << LO) * t.j20;
             small[i] = ex ? pass_root_pow(a, ex) : 1;
@@ -471,7 +473,7 @@ __host__ __device__ __forceinline__ void pass_tables_tab(const PassTile& t, uint
 {
     if (ROLE != kRoleTable || S <= 3) return;
     constexpr uint32_t LO = pass_tab_lo_lg<S>();
-    const uint64_t* small = lds + pass_wtab_offset<S, ROLE>(t.logV) + kW512Words;
+    const uint64_t* small = lds;
     uint64_t* tab = lds + ((1u << S) << t.logV);
     for (uint32_t i = tid; i < (1u << S); i += T)
         tab[i] = gl_mul(small[i & ((1u << LO) - 1)], small[(1u << LO) + (i >> LO)]);

@@ -15,6 +15,11 @@ constexpr uint32_t kMaxPassBits = 9;
 #define ZK_NTT_THREADS 512
 #endif
 constexpr uint32_t kNttThreads = ZK_NTT_THREADS;
+// log2 of the tile's vector lanes V (columns times j2 values per tile).
+#ifndef ZK_NTT_LOGV
+#define ZK_NTT_LOGV 4
+#endif
+constexpr uint32_t kNttLogV = ZK_NTT_LOGV;
 constexpr uint64_t kW512Len = 1ull << kStepTableLg;  // w_512^k, k < 512
 constexpr uint64_t kBigLen = 1ull << 16;             // two-level table of w_{2^32}
 constexpr uint64_t kTableLen = 2 * kW512Len + 4 * kBigLen;
@@ -68,7 +73,7 @@ inline Plan make_plan(uint32_t L, uint64_t w)
     Plan p;
     p.L = L;
     uint32_t logC = 0;
-    while (logC < 4 && (w % (2ull << logC)) == 0) logC++;
+    while (logC < kNttLogV && (w % (2ull << logC)) == 0) logC++;
     p.logC = logC;
     p.np = L == 0 ? 0 : (L + kMaxPassBits - 1) / kMaxPassBits;
     for (uint32_t i = 0; i < p.np; i++) p.sb[i] = L / p.np + (i < L % p.np ? 1 : 0);
@@ -121,7 +126,7 @@ inline PassArgs pass_args(const Plan& p, uint32_t i, uint32_t B, uint64_t w, con
     a.s = p.sb[i];
     a.logC = p.logC;
     const uint32_t logN2 = B - a.s;
-    uint32_t logJ = 4 - p.logC;
+    uint32_t logJ = kNttLogV - p.logC;
     if (logJ > logN2) logJ = logN2;
     a.logJ = logJ;
     a.last = last ? 1 : 0;
@@ -153,10 +158,7 @@ inline size_t pass_lds_bytes(const PassArgs& a)
 {
     if (a.s <= 3) return 0;
     size_t words = (size_t)1 << (a.s + a.logC + a.logJ);
-    if (pass_uses_twtab(a)) {
-        const uint32_t lo = a.s < kTabLoLg ? a.s : kTabLoLg;
-        words += ((size_t)1 << a.s) + ((size_t)1 << lo) + ((size_t)1 << (a.s - lo));
-    }
+    if (pass_uses_twtab(a)) words += (size_t)1 << a.s;
     words += kW512Words;
     return words * 8;
 }
