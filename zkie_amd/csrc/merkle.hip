@@ -5,8 +5,9 @@
 //  * one row (leaf) or one parent (compression) per lane, so a wave of 64
 //    lanes runs 64 independent permutations; the reference kernel instead
 //    hashes 8 rows serially per thread (poseidon2_merkle.cu:187-196);
-//  * the upper tree levels, where a level has too few parents to fill the
-//    GPU, are reduced by one workgroup per subtree inside LDS (a level per
+//  * levels with few parents, whose time is one permutation's latency, run
+//    one permutation per 16-lane row (poseidon2_x16.hpp), and the top levels
+//    of the tree are reduced by one workgroup inside LDS (a level per
 //    barrier) instead of one kernel launch per level (merkle_cuda.rs:250-280);
 //  * the digest layers stay in HBM; openings gather rows and siblings on the
 //    device and copy only what was asked for.
@@ -15,6 +16,7 @@
 #include <vector>
 
 #include "poseidon2.hpp"
+#include "poseidon2_x16.hpp"
 #include "row_stage.hpp"
 #include "runtime.hpp"
 
@@ -78,10 +80,12 @@ void derive_default(P2Consts& c)
     c.diag15 = INV_2_32;
 }
 
-int upload(const P2Consts& c)
+int upload(const P2Consts& in)
 {
     const int dev = current_device();
     if (dev < 0 || dev >= kMaxDevices) return ZKIE_ERR_INVALID;
+    P2Consts c = in;
+    p2_set_diag(c);
     ZK_TRY(hipMemcpyToSymbol(HIP_SYMBOL(c_p2), &c, sizeof(P2Consts), 0, hipMemcpyHostToDevice));
     g_uploaded[dev] = true;
     g_diag_fast[dev] = gl_canon(c.diag15) == INV_2_32;
@@ -220,44 +224,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     store_digest(next + i * 8, st);
 }
 
+// compress_kernel for levels with few parents: one parent per 16-lane row,
+// lane i holding state word i (the 16 words of two adjacent children are
+// contiguous). Same slots and zero padding as compress_kernel; a row's lanes
+// always take the same path.
+__global__ __launch_bounds__(256) void compress_x16_kernel(const uint64_t* __restrict__ prev,
+                                                           uint64_t* __restrict__ next, uint64_t from,
+                                                           uint64_t to, uint64_t pad_to, uint32_t step)
+{
+    const uint64_t p = from + ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / 16;
+    const uint32_t i = threadIdx.x & 15;
+    if (p >= pad_to) return;
+    if (p >= to) {
+        if (i < 8) next[p * 8 + i] = 0;
+        return;
+    }
+    uint64_t x;
+    if (step == 2)
+        x = prev[p * 16 + i];
+    else
+        x = i < 8 ? prev[p * 8 + i] : 0;
+    const X16Lane L = x16_lane(c_p2, i);
+    x = p2_permute_x16(x, L, c_p2);
+    if (i < 8) next[p * 8 + i] = gl_canon(x);
+}
+
 // One workgroup reduces 2^levels consecutive digests of a layer to one
 // digest, writing every intermediate layer: the top of the tree in LDS, one
-// level per barrier. Parent j of level t (t = 1..levels) of subtree g is
-// written to out_layers[t-1] + (g << (levels - t)) + j.
+// level per barrier, one parent per 16-lane row. Parent j of level t
+// (t = 1..levels) of subtree g is written to out_layers[t-1] +
+// (g << (levels - t)) + j.
+constexpr uint32_t kSubLevels = 7;  // at most 128 digests: 64 parents, one row each
+constexpr uint32_t kSubThreads = 1024;
 struct SubtreeArgs {
     const uint64_t* in;    // first layer (already computed), 2^levels * groups digests
     uint64_t* out[24];     // output layer base pointers, level 1..levels
     uint32_t levels;
 };
 
-template <bool D15>
-__global__ __launch_bounds__(256) void subtree_kernel(SubtreeArgs a)
+__global__ __launch_bounds__(kSubThreads) void subtree_kernel(SubtreeArgs a)
 {
-    __shared__ uint64_t lds[256 * 8];  // up to 256 digests of the current level
+    // level t's digests in buf[t & 1]; level t + 1 reads them after the barrier
+    __shared__ uint64_t buf[2][(1u << (kSubLevels - 1)) * 8];
     const uint32_t g = blockIdx.x;
-    const uint32_t tid = threadIdx.x;
-    uint32_t n = 1u << a.levels;       // digests at the current level (<= 512)
+    const uint32_t row = threadIdx.x / 16, i = threadIdx.x & 15, rows = blockDim.x / 16;
+    const X16Lane L = x16_lane(c_p2, i);
     const uint64_t* src = a.in + ((uint64_t)g << a.levels) * 8;
-    // Level 1 reads its children straight from the input layer.
+    uint32_t n = 1u << a.levels;
     for (uint32_t t = 1; t <= a.levels; t++) {
         const uint32_t parents = n >> 1;
-        uint64_t st[16];
-        const bool active = tid < parents;
-        if (active) {
-            if (t == 1) {
-                load8(st, src + (uint64_t)(2 * tid) * 8);
-                load8(st + 8, src + (uint64_t)(2 * tid + 1) * 8);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 16; k++) st[k] = lds[(2 * tid) * 8 + k];
+        for (uint32_t p = row; p < parents; p += rows) {
+            uint64_t x = t == 1 ? src[16 * p + i] : buf[(t - 1) & 1][16 * p + i];
+            x = p2_permute_x16(x, L, c_p2);
+            if (i < 8) {
+                const uint64_t c = gl_canon(x);
+                buf[t & 1][8 * p + i] = c;
+                a.out[t - 1][(((uint64_t)g << (a.levels - t)) + p) * 8 + i] = c;
             }
-            p2_permute<D15>(st, c_p2);
-        }
-        __syncthreads();
-        if (active) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) lds[tid * 8 + k] = gl_canon(st[k]);
-            store_digest(a.out[t - 1] + (((uint64_t)g << (a.levels - t)) + tid) * 8, st);
         }
         __syncthreads();
         n = parents;
@@ -307,16 +330,23 @@ int launch_leaves(const uint64_t* mat, uint64_t* dig, uint64_t r0, uint64_t r1, 
     return ZKIE_OK;
 }
 
+// Up to this many parent slots a level runs one permutation per 16-lane row:
+// below it, a launch with one permutation per lane takes the latency of one
+// permutation whatever its size, and the row form has a fifth of that
+// latency for about three times the instructions.
+constexpr uint64_t kX16MaxParents = 1ull << 15;
+
 int launch_compress(const uint64_t* prev, uint64_t* next, uint64_t from, uint64_t to,
                     uint64_t pad_to, uint32_t step, bool fast, hipStream_t s)
 {
     if (pad_to <= from) return ZKIE_OK;
-    const unsigned grid = grid_for(pad_to - from);
     ProfMark m = prof_begin("p2_compress", s);
-    if (fast)
-        compress_kernel<true><<<grid, 256, 0, s>>>(prev, next, from, to, pad_to, step);
+    if (pad_to - from <= kX16MaxParents)
+        compress_x16_kernel<<<grid_for((pad_to - from) * 16), 256, 0, s>>>(prev, next, from, to, pad_to, step);
+    else if (fast)
+        compress_kernel<true><<<grid_for(pad_to - from), 256, 0, s>>>(prev, next, from, to, pad_to, step);
     else
-        compress_kernel<false><<<grid, 256, 0, s>>>(prev, next, from, to, pad_to, step);
+        compress_kernel<false><<<grid_for(pad_to - from), 256, 0, s>>>(prev, next, from, to, pad_to, step);
     prof_end(m, s);
     ZK_LAUNCHED();
     return ZKIE_OK;
@@ -356,8 +386,7 @@ int build_upper(uint64_t* d_layers, const std::vector<uint64_t>& lens, bool fast
         // Subtree path: a power-of-two layer of at most 2^kSub digests
         // reduces to the root in one launch (all levels above are exact
         // halvings, no padding).
-        constexpr uint32_t kSub = 9;  // 512 digests -> 256 parents in LDS
-        if ((len & (len - 1)) == 0 && len <= (1ull << kSub) && len >= 2) {
+        if ((len & (len - 1)) == 0 && len <= (1ull << kSubLevels) && len >= 2) {
             SubtreeArgs a;
             a.in = d_layers + off[i];
             uint32_t levels = 0;
@@ -365,10 +394,7 @@ int build_upper(uint64_t* d_layers, const std::vector<uint64_t>& lens, bool fast
             a.levels = levels;
             for (uint32_t t = 1; t <= levels; t++) a.out[t - 1] = d_layers + off[i + t];
             ProfMark m = prof_begin("p2_subtree", s);
-            if (fast)
-                subtree_kernel<true><<<1, 256, 0, s>>>(a);
-            else
-                subtree_kernel<false><<<1, 256, 0, s>>>(a);
+            subtree_kernel<<<1, kSubThreads, 0, s>>>(a);
             prof_end(m, s);
             ZK_LAUNCHED();
             return ZKIE_OK;

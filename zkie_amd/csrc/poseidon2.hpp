@@ -36,7 +36,18 @@ struct P2Consts {
     uint64_t ext[8][16];  // [0..4) initial, [4..8) terminal external rounds
     uint64_t internal[22];
     uint64_t diag15;
+    uint64_t diag[16];  // the whole internal diagonal V (p2_set_diag)
 };
+
+// V = [-2, 1, 2, 1/2, 3, 4, -1/2, -3, -4, 1/2^3, 1/2^4, 1/2^5, -1/2^3,
+// -1/2^4, -1/2^5, diag15] (poseidon2_merkle.cu:111-142), canonical.
+inline void p2_set_diag(P2Consts& c)
+{
+    const uint64_t i2 = gl_inv(2), i8 = gl_inv(8), i16 = gl_inv(16), i32 = gl_inv(32);
+    const uint64_t V[16] = {P - 2, 1, 2, i2, 3, 4, P - i2, P - 3, P - 4, i8, i16, i32, P - i8, P - i16, P - i32,
+                            gl_canon(c.diag15)};
+    for (int i = 0; i < 16; i++) c.diag[i] = V[i];
+}
 
 __host__ __device__ __forceinline__ uint64_t sbox7(uint64_t x)
 {
