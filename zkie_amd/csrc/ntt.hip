@@ -45,7 +45,7 @@ int ensure_tables(const uint64_t** out)
     return ZKIE_OK;
 }
 
-template <int S, int KNZ, bool INV, int ROLE, int LOGV>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV, int ROWS>
 __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 {
     extern __shared__ uint64_t lds[];
@@ -53,6 +53,7 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
     // the step loops unroll to their exact number of rounds.
     constexpr uint32_t T = kNttThreads;
     const uint32_t tid = threadIdx.x;
+    __builtin_assume(tid < T);  // lets the step loops drop their item-count checks
     constexpr int n = pass_steps<S>();
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
     const PassTile t = pass_tile(a, bid);
@@ -61,14 +62,23 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
         pass_step<S, KNZ, INV, ROLE, LOGV>(0, a, t, l, tid, T, lds);
     } else {
         static_assert(((1u << (S - Radix<S>::r0)) << kNttLogV) <= kStepU * T, "step 0 in one round");
-        // The tile's HBM reads go out first; the twiddle tables are filled in
-        // LDS while they are in flight, so the latencies overlap.
+        // The table words are read first and the tile right after; the
+        // tables are written to LDS (and the inter-pass table formed) while
+        // the tile is still in flight, so the latencies overlap. The code is
+        // straight-line from the table loads to their LDS writes (the row
+        // check is a template choice), so the wait before the writes counts
+        // the tile's loads as still in flight.
+        static_assert(pass_table_entries<S, ROLE>() <= T, "a thread per table entry");
+        const PassTabFetch tf = pass_tables_fetch<S, ROLE>(a, t, tid);
+        __builtin_amdgcn_sched_barrier(0);  // keep the table loads ahead of the tile's
         uint64_t x[kStepU][1 << Radix<S>::r0];
-        pass_step0_gather<S, KNZ, LOGV>(a, t, l, tid, T, x);
-        pass_tables<S, ROLE>(a, t, tid, T, lds);
-        __syncthreads();
-        pass_tables_tab<S, ROLE>(t, tid, T, lds);
+        pass_step0_gather<S, KNZ, LOGV, ROWS>(a, t, l, tid, T, x);
+        pass_tables_put<S, ROLE>(tf, t, tid, lds);
         __syncthreads();  // step twiddles in LDS before step 0 reads them
+        if constexpr (ROLE == kRoleTable) {
+            pass_tables_tab<S, ROLE>(t, tid, T, lds);
+            __syncthreads();  // small tables read before step 0 overwrites them
+        }
         pass_step0_finish<S, KNZ, INV, ROLE, LOGV>(a, t, l, tid, T, lds, x);
         __syncthreads();
         pass_step<S, KNZ, INV, ROLE, LOGV>(1, a, t, l, tid, T, lds);
@@ -82,12 +92,12 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 // Launch one instantiation, one workgroup per tile; dynamic LDS above the
 // 64 KB default needs the kernel's limit raised first (gfx950 has 160 KB of
 // LDS per CU).
-template <int S, int KNZ, bool INV, int ROLE, int LOGV>
+template <int S, int KNZ, bool INV, int ROLE, int LOGV, int ROWS>
 hipError_t launch_one(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
 {
     static size_t raised = 64 * 1024;
     if (shmem > raised) {
-        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV>,
+        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV, ROWS>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
         if (e != hipSuccess) return e;
         raised = shmem;
@@ -100,16 +110,30 @@ hipError_t launch_one(const PassArgs& a, uint64_t blocks, size_t shmem, hipStrea
         if ((blocks % gx) != 0) return hipErrorInvalidValue;
         grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
     }
-    ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV><<<grid, kNttThreads, shmem, s>>>(a);
+    ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV, ROWS><<<grid, kNttThreads, shmem, s>>>(a);
     return hipGetLastError();
+}
+
+// A first pass whose input has fewer rows than its read pattern covers
+// checks rows (a separate instance); every other pass reads whole tiles. A
+// pass reading all R inputs of its step-0 items (KNZ = 8) covers exactly the
+// input's rows.
+template <int S, int KNZ, bool INV, int ROLE, int LOGV>
+hipError_t launch_rows(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
+{
+    if (!a.check_rows) return launch_one<S, KNZ, INV, ROLE, LOGV, kRowsAll>(a, blocks, shmem, s);
+    if constexpr (KNZ < 8 && !INV)
+        return launch_one<S, KNZ, INV, ROLE, LOGV, kRowsChecked>(a, blocks, shmem, s);
+    else
+        return hipErrorInvalidValue;
 }
 
 // Tiles of 16 vector lanes (the usual case) address LDS with immediate offsets.
 template <int S, int KNZ, bool INV, int ROLE>
 hipError_t launch_v(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
 {
-    if (a.logC + a.logJ == kNttLogV) return launch_one<S, KNZ, INV, ROLE, (int)kNttLogV>(a, blocks, shmem, s);
-    return launch_one<S, KNZ, INV, ROLE, -1>(a, blocks, shmem, s);
+    if (a.logC + a.logJ == kNttLogV) return launch_rows<S, KNZ, INV, ROLE, (int)kNttLogV>(a, blocks, shmem, s);
+    return launch_rows<S, KNZ, INV, ROLE, -1>(a, blocks, shmem, s);
 }
 
 // Instances: forward passes prune zero inputs of an LDE (KNZ < 8) and never

@@ -276,7 +276,12 @@ constexpr int kStepU = 2;
 // non-zero, the rest are the zero padding of an LDE), else from the LDS tile.
 // LOGV is the tile's log2 vector width when known at compile time (then LDS
 // addresses are a base plus immediate offsets), or -1 to read it from the tile.
-template <int S, int RL, int BS, int KNZ, bool FROM_GLOBAL, int LOGV>
+// ROWS (FROM_GLOBAL): kRowsAll when every input row exists (a.check_rows
+// clear), kRowsChecked when rows past the input read as zero, kRowsAny to
+// decide at run time.
+enum { kRowsAny = 0, kRowsAll = 1, kRowsChecked = 2 };
+
+template <int S, int RL, int BS, int KNZ, bool FROM_GLOBAL, int LOGV, int ROWS = kRowsAny>
 __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const PassTile& t, const PassLane& l,
                                                      uint32_t it0, uint32_t T, const uint64_t* lds,
                                                      uint64_t (&x)[kStepU][1 << RL])
@@ -286,6 +291,30 @@ __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const Pa
     const uint32_t logV = LOGV >= 0 ? (uint32_t)LOGV : t.logV;
     const uint32_t items = (1u << (S - RL)) << logV;
     const uint32_t v = l.v;
+    if (FROM_GLOBAL && ROWS != kRowsChecked && (ROWS == kRowsAll || !a.check_rows)) {
+        // Every input row exists: straight-line loads with no branch or
+        // select after them, so that a later wait for an older load (the
+        // LDS tables) can leave the whole tile in flight.
+#pragma unroll
+        for (int u = 0; u < kStepU; u++) {
+            const uint32_t it = it0 + (uint32_t)u * T;
+            if (it >= items) continue;
+            uint32_t base, q;
+            step_item<RL, BS>(it, logV, base, q);
+            const uint64_t gbase = l.in_base + (uint64_t)base * a.in_stride;
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+                if (k < KNZ) {
+                    const uint64_t idx = gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride;
+                    ZK_BOUND(idx, a.in_len);
+                    x[u][k] = a.in[idx];
+                } else {
+                    x[u][k] = 0;
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < kStepU; u++) {
         const uint32_t it = it0 + (uint32_t)u * T;
@@ -298,10 +327,14 @@ __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const Pa
         for (int k = 0; k < R; k++) {
             const uint32_t pos = base + ((uint32_t)k << QL);
             if (FROM_GLOBAL) {
-                if (k < KNZ && (!a.check_rows || pos < l.pos_lim)) {
-                    const uint64_t idx = gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride;
+                if (k < KNZ) {
+                    // A row past the input reads element 0 and keeps 0: the
+                    // same number of loads as the straight-line form above.
+                    const bool in = pos < l.pos_lim;
+                    const uint64_t idx = in ? gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride : 0;
                     ZK_BOUND(idx, a.in_len);
-                    x[u][k] = a.in[idx];
+                    const uint64_t val = a.in[idx];
+                    x[u][k] = in ? val : 0;
                 } else {
                     x[u][k] = 0;
                 }
@@ -444,25 +477,65 @@ __host__ __device__ __forceinline__ constexpr uint32_t pass_tab_lo_lg()
 }
 
 // Before step 0, first half (a barrier follows): the step twiddles w_512^k
-// into LDS and, for kRoleTable, the two small power tables.
+// into LDS and, for kRoleTable, the two small power tables. Entry i comes
+// from pass_tables_fetch (its HBM words) and pass_tables_put (the LDS
+// write), so that a kernel with a thread per entry can issue these loads
+// before its tile's and write the tables while the tile is still in flight.
+struct PassTabFetch {
+    uint64_t w;       // w_512^i
+    uint64_t r0, r1;  // the two root-table factors of small-table entry i (1, 1 for w^0 or none)
+};
+
+template <int S, int ROLE>
+__host__ __device__ __forceinline__ PassTabFetch pass_tables_fetch(const PassArgs& a, const PassTile& t,
+                                                                   uint32_t i)
+{
+    // No branch around the loads (entries past the tables read w^0 = lo[0]
+    // hi[0] = 1), so a kernel's later wait for them can leave its tile's
+    // loads in flight.
+    PassTabFetch f{0, 1, 1};
+    if (S <= 3) return f;
+    if (i < kW512Words) f.w = a.w512[i];
+    if (ROLE == kRoleTable) {
+        constexpr uint32_t LO = pass_tab_lo_lg<S>();
+        constexpr uint32_t nlo = 1u << LO, nhi = 1u << (S - LO);
+        const uint64_t ex =
+            i < nlo + nhi ? (i < nlo ? (uint64_t)i : (uint64_t)(i - nlo) << LO) * t.j20 : 0;
+        const uint64_t E = ex << (32 - a.B);  // w_{2^B}^ex = lo[E mod 2^16] hi[E >> 16]
+        f.r0 = a.twlo[E & 0xFFFF];
+        f.r1 = a.twhi[E >> 16];
+    }
+    return f;
+}
+
+template <int S, int ROLE>
+__host__ __device__ __forceinline__ void pass_tables_put(const PassTabFetch& f, const PassTile& t, uint32_t i,
+                                                         uint64_t* lds)
+{
+    if (S <= 3) return;
+    if (i < kW512Words) lds[pass_wtab_offset<S, ROLE>(t.logV) + i] = f.w;
+    if (ROLE == kRoleTable) {
+        constexpr uint32_t LO = pass_tab_lo_lg<S>();
+        constexpr uint32_t nlo = 1u << LO, nhi = 1u << (S - LO);
+        static_assert(S <= 3 || nlo + nhi <= (1u << S), "small tables fit the tile region");
+        if (i < nlo + nhi) lds[i] = gl_mul(f.r0, f.r1);  // [lo | hi], in the tile region
+    }
+}
+
+// Entries needed per workgroup (a thread per entry in the kernel).
+template <int S, int ROLE>
+__host__ __device__ __forceinline__ constexpr uint32_t pass_table_entries()
+{
+    return ROLE == kRoleTable && (1u << S) > kW512Words ? (1u << S) : kW512Words;
+}
+
 template <int S, int ROLE>
 __host__ __device__ __forceinline__ void pass_tables(const PassArgs& a, const PassTile& t, uint32_t tid,
                                                      uint32_t T, uint64_t* lds)
 {
     if (S <= 3) return;
-    uint64_t* wtab = lds + pass_wtab_offset<S, ROLE>(t.logV);
-    for (uint32_t i = tid; i < kW512Words; i += T) wtab[i] = a.w512[i];
-    if (ROLE == kRoleTable) {
-        constexpr uint32_t LO = pass_tab_lo_lg<S>();
-        constexpr uint32_t nlo = 1u << LO, nhi = 1u << (S - LO);
-        uint64_t* small = lds;  // [lo | hi], in the tile region
-        static_assert(S <= 3 || (1u << pass_tab_lo_lg<S>()) + (1u << (S - pass_tab_lo_lg<S>())) <= (1u << S),
-                      "small tables fit the tile region");
-        for (uint32_t i = tid; i < nlo + nhi; i += T) {
-            const uint64_t ex = (i < nlo ? (uint64_t)i : (uint64_t)(i - nlo) << LO) * t.j20;
-            small[i] = ex ? pass_root_pow(a, ex) : 1;
-        }
-    }
+    for (uint32_t i = tid; i < pass_table_entries<S, ROLE>(); i += T)
+        pass_tables_put<S, ROLE>(pass_tables_fetch<S, ROLE>(a, t, i), t, i, lds);
 }
 
 // Before step 0, second half (after a barrier; a barrier separates it from
@@ -508,12 +581,12 @@ __host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, con
 // Step 0 of a multi-step pass in two halves, so that a kernel can issue its
 // HBM reads before the LDS tables are filled: the reads of all items (one
 // round: 2^(S - r0) V <= kStepU T) and, after a barrier, the rest.
-template <int S, int KNZ, int LOGV>
+template <int S, int KNZ, int LOGV, int ROWS = kRowsAny>
 __host__ __device__ __forceinline__ void pass_step0_gather(const PassArgs& a, const PassTile& t,
                                                            const PassLane& l, uint32_t tid, uint32_t T,
                                                            uint64_t (&x)[kStepU][1 << Radix<S>::r0])
 {
-    step_gather<S, Radix<S>::r0, S, KNZ, true, LOGV>(a, t, l, tid, T, nullptr, x);
+    step_gather<S, Radix<S>::r0, S, KNZ, true, LOGV, ROWS>(a, t, l, tid, T, nullptr, x);
 }
 
 template <int S, int KNZ, bool INV, int ROLE, int LOGV>
