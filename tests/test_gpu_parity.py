@@ -106,6 +106,30 @@ def test_reference_p2_entries(native, oracle, h, w):
         assert (d.download().reshape(-1, 8) == o).all()
 
 
+@pytest.mark.parametrize("parents,step", [(24, 1), (1003, 1), (40000, 1), (1000, 2), (1 << 15, 2),
+                                          ((1 << 15) + 13, 2)])
+def test_compress_entries_one_and_two_children(native, oracle, parents, step):
+    """zkie_p2_compress_batch/_scalar with one child per parent (the child in
+    words 0..7, zeros after, poseidon2_merkle.cu:214-221) and with two, on
+    both sides of the size where a level switches from one permutation per
+    lane to one per 16-lane row."""
+    _case("compress entries", parents, step)
+    L = native.load()
+    prev = oracle.gen_uniform(parents + step, parents * step * 8).reshape(parents * step, 8)
+    d_prev = DeviceBuffer.from_array(prev)
+    d_next = DeviceBuffer(parents * 8)
+    end = parents // 8 * 8
+    check(L.zkie_p2_compress_batch(d_prev.addr, d_next.addr, parents, step), "compress_batch")
+    check(L.zkie_p2_compress_scalar(d_prev.addr, d_next.addr, end, parents, step), "compress_scalar")
+    check(L.zkie_device_synchronize(), "sync")
+    got = d_next.download().reshape(parents, 8)
+    st = np.zeros(16, np.uint64)
+    for r in range(parents):
+        st[:] = 0
+        st[: 8 * step] = prev[step * r: step * r + step].reshape(-1)
+        assert (got[r] == oracle.p2_permute(st)[:8] % np.uint64(P)).all(), r
+
+
 def test_openings(native, oracle):
     _case("openings")
     h, w = 1000, 16
