@@ -383,21 +383,26 @@ int build_upper(uint64_t* d_layers, const std::vector<uint64_t>& lens, bool fast
     const size_t top = lens.size() - 1;
     while (i < top) {
         const uint64_t len = lens[i];
-        // Subtree path: a power-of-two layer of at most 2^kSub digests
-        // reduces to the root in one launch (all levels above are exact
-        // halvings, no padding).
-        if ((len & (len - 1)) == 0 && len <= (1ull << kSubLevels) && len >= 2) {
+        // Subtree path: every level above a power-of-two layer is an exact
+        // halving (no padding), so a layer of at most 2^kSubLevels digests
+        // reduces to the root in one launch, and a layer of at most
+        // kX16MaxParents * 2 digests loses kSubLevels levels in one launch of
+        // one workgroup per 2^kSubLevels-digest subtree.
+        if ((len & (len - 1)) == 0 && len >= 2 && len <= 2 * kX16MaxParents) {
+            uint32_t lg = 0;
+            while ((1ull << lg) < len) lg++;
+            const uint32_t levels = lg < kSubLevels ? lg : kSubLevels;
             SubtreeArgs a;
             a.in = d_layers + off[i];
-            uint32_t levels = 0;
-            while ((1ull << levels) < len) levels++;
             a.levels = levels;
             for (uint32_t t = 1; t <= levels; t++) a.out[t - 1] = d_layers + off[i + t];
+            const unsigned groups = (unsigned)(len >> levels);
             ProfMark m = prof_begin("p2_subtree", s);
-            subtree_kernel<<<1, kSubThreads, 0, s>>>(a);
+            subtree_kernel<<<groups, kSubThreads, 0, s>>>(a);
             prof_end(m, s);
             ZK_LAUNCHED();
-            return ZKIE_OK;
+            i += levels;
+            continue;
         }
         const uint64_t raw = len / 2;
         int rc = launch_compress(d_layers + off[i], d_layers + off[i + 1], 0, raw, lens[i + 1], 2,
