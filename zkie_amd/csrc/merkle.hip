@@ -6,9 +6,10 @@
 //    lanes runs 64 independent permutations; the reference kernel instead
 //    hashes 8 rows serially per thread (poseidon2_merkle.cu:187-196);
 //  * levels with few parents, whose time is one permutation's latency, run
-//    one permutation per 16-lane row (poseidon2_x16.hpp), and the top levels
-//    of the tree are reduced by one workgroup inside LDS (a level per
-//    barrier) instead of one kernel launch per level (merkle_cuda.rs:250-280);
+//    one permutation per 16-lane row (poseidon2_x16.hpp), and above a
+//    power-of-two layer of at most 2^16 digests seven levels at a time are
+//    reduced by one workgroup per subtree inside LDS (a level per barrier)
+//    instead of one kernel launch per level (merkle_cuda.rs:250-280);
 //  * the digest layers stay in HBM; openings gather rows and siblings on the
 //    device and copy only what was asked for.
 #include <algorithm>
