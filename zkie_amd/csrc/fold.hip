@@ -154,8 +154,9 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
         ZK_LAUNCHED();
         return ZKIE_OK;
     }
-    uint64_t* d_eq = (uint64_t*)workspace(WS_MISC, eq.size() * 8);
-    if (!d_eq) return ZKIE_ERR_ALLOC;
+    Scratch ws(WS_MISC, eq.size() * 8, s);
+    if (ws.status()) return ws.status();
+    uint64_t* d_eq = (uint64_t*)ws.get();
     ZK_TRY(hipMemcpyAsync(d_eq, eq.data(), eq.size() * 8, hipMemcpyHostToDevice, s));
     ProfMark m = prof_begin("fold_rows", s);
     if (is_ext)
@@ -164,7 +165,7 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
         fold_kernel_rt<false><<<grid, 256, 0, s>>>(d_mat, h, k, d_eq, d_out);
     prof_end(m, s);
     ZK_LAUNCHED();
-    // The eq buffer is shared workspace: finish before a later call reuses it.
+    // The eq weights were copied from a host vector that ends with this call.
     ZK_TRY(hipStreamSynchronize(s));
     return ZKIE_OK;
 }
@@ -197,8 +198,9 @@ int mle_eval_device(const uint64_t* d_vals, uint32_t t, int is_ext, const uint64
     }
     const uint32_t k0 = t < 6 ? t : 6;
     const uint64_t first = 1ull << (t - k0);  // EF entries after the first fold
-    uint64_t* buf = (uint64_t*)workspace(WS_FOLD, 2 * first * 16);
-    if (!buf) return ZKIE_ERR_ALLOC;
+    Scratch ws(WS_FOLD, 2 * first * 16, s);
+    if (ws.status()) return ws.status();
+    uint64_t* buf = (uint64_t*)ws.get();
     uint64_t* ping = buf;
     uint64_t* pong = buf + 2 * first;
     const uint64_t* cur = d_vals;
@@ -228,8 +230,9 @@ int fold_rows_at_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ex
     for (uint64_t i = 0; i < n; i++)
         if (ids[i] >= h) return ZKIE_ERR_INVALID;
     const uint64_t width = (is_ext ? 2ull : 1ull) << k;
-    uint64_t* buf = (uint64_t*)workspace(WS_FOLD, (n + n * width + 2 * n) * 8);
-    if (!buf) return ZKIE_ERR_ALLOC;
+    Scratch ws(WS_FOLD, (n + n * width + 2 * n) * 8, s);
+    if (ws.status()) return ws.status();
+    uint64_t* buf = (uint64_t*)ws.get();
     uint64_t* d_ids = buf;
     uint64_t* d_rows = buf + n;
     uint64_t* d_out = d_rows + n * width;

@@ -545,8 +545,9 @@ int gather_to_host(const uint64_t* d_src, uint64_t stride, uint64_t len,
     if (ids.empty() || len == 0) return ZKIE_OK;
     const uint64_t count = ids.size();
     const size_t bytes_ids = count * 8, bytes_out = count * len * 8;
-    uint8_t* ws = (uint8_t*)workspace(WS_MISC, bytes_ids + bytes_out);
-    if (!ws) return ZKIE_ERR_ALLOC;
+    Scratch lease(WS_MISC, bytes_ids + bytes_out, s);
+    if (lease.status()) return lease.status();
+    uint8_t* ws = (uint8_t*)lease.get();
     uint64_t* d_ids = (uint64_t*)ws;
     uint64_t* d_out = (uint64_t*)(ws + bytes_ids);
     ZK_TRY(hipMemcpyAsync(d_ids, ids.data(), bytes_ids, hipMemcpyHostToDevice, s));

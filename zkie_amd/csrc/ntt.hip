@@ -226,11 +226,10 @@ int dft_inplace(uint64_t* d_mat, uint64_t* d_tmp, uint32_t lg, uint64_t w, bool 
     if (!plan_fits(p, w)) return ZKIE_ERR_INVALID;
     const uint64_t n = 1ull << lg;
     if (p.np == 1) return run_passes(p, w, d_mat, n, nullptr, d_mat, inverse, s);
-    if (!d_tmp) {
-        d_tmp = (uint64_t*)workspace(WS_NTT, n * w * 8);
-        if (!d_tmp) return ZKIE_ERR_ALLOC;
-    }
-    return run_passes(p, w, d_mat, n, d_tmp, d_mat, inverse, s);
+    if (d_tmp) return run_passes(p, w, d_mat, n, d_tmp, d_mat, inverse, s);
+    Scratch ws(WS_NTT, n * w * 8, s);
+    if (ws.status()) return ws.status();
+    return run_passes(p, w, d_mat, n, (uint64_t*)ws.get(), d_mat, inverse, s);
 }
 
 }  // namespace
@@ -264,14 +263,15 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
             tab[kBigLen + k] = x;
             x = gl_canon(gl_mul(x, step));
         }
-        uint64_t* d_tab = (uint64_t*)workspace(WS_MISC, tab.size() * 8);
-        if (!d_tab) return ZKIE_ERR_ALLOC;
+        Scratch ws(WS_MISC, tab.size() * 8, s);  // released before the WS_NTT lease below
+        if (ws.status()) return ws.status();
+        uint64_t* d_tab = (uint64_t*)ws.get();
         ZK_TRY(hipMemcpyAsync(d_tab, tab.data(), tab.size() * 8, hipMemcpyHostToDevice, s));
         const uint64_t total = h * w;
         coset_scale_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(d_in, d_out, h, w, d_tab,
                                                                           d_tab + kBigLen);
         ZK_LAUNCHED();
-        ZK_TRY(hipStreamSynchronize(s));  // the table buffer is reused by later calls
+        ZK_TRY(hipStreamSynchronize(s));  // the table was copied from a host vector
         src = d_out;
     }
     if (p.np == 1) {
@@ -281,9 +281,9 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
         }
         return run_passes(p, w, src, h, nullptr, d_out, false, s);
     }
-    uint64_t* tmp = (uint64_t*)workspace(WS_NTT, n * w * 8);
-    if (!tmp) return ZKIE_ERR_ALLOC;
-    return run_passes(p, w, src, h, tmp, d_out, false, s);
+    Scratch ws(WS_NTT, n * w * 8, s);
+    if (ws.status()) return ws.status();
+    return run_passes(p, w, src, h, (uint64_t*)ws.get(), d_out, false, s);
 }
 
 // Prefix order (writer.rs:43-71): entry (i, j) of the committed matrix, row

@@ -19,13 +19,19 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 
-struct Workspace {
+}  // namespace
+
+struct ScratchSlot {
+    std::mutex mu;              // held for the whole of a lease
     void* ptr = nullptr;
     size_t bytes = 0;
+    hipEvent_t done = nullptr;  // recorded on the last lease's stream when it ended
+    bool pending = false;       // `done` marks GPU work that may still use ptr
 };
 
-Workspace g_ws[kMaxDevices][WS_COUNT];
-std::mutex g_ws_mu;
+namespace {
+
+ScratchSlot g_slots[kMaxDevices][WS_COUNT];
 
 struct ProfRecord {
     int kernel;
@@ -78,25 +84,61 @@ void prof_drain(ProfState& P)
 
 }  // namespace
 
-void* workspace(WorkspaceSlot slot, size_t bytes)
+Scratch::Scratch(WorkspaceSlot slot, size_t bytes, hipStream_t s) : s_(s)
 {
     const int dev = current_device();
-    if (dev < 0 || dev >= kMaxDevices) return nullptr;
-    std::lock_guard<std::mutex> g(g_ws_mu);
-    Workspace& w = g_ws[dev][slot];
-    if (w.bytes >= bytes && w.ptr) return w.ptr;
-    if (w.ptr) {
-        // The previous buffer may still be read by queued kernels.
-        if (hipDeviceSynchronize() != hipSuccess) return nullptr;
-        (void)hipFree(w.ptr);
-        w.ptr = nullptr;
-        w.bytes = 0;
+    if (dev < 0 || dev >= kMaxDevices || slot < 0 || slot >= WS_COUNT) {
+        rc_ = ZKIE_ERR_NO_DEVICE;
+        return;
     }
-    void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
-    w.ptr = p;
-    w.bytes = bytes;
-    return p;
+    ScratchSlot& w = g_slots[dev][slot];
+    w.mu.lock();
+    slot_ = &w;
+    if (!w.ptr || w.bytes < bytes) {
+        if (w.ptr) {
+            // Queued kernels of earlier leases may still use the old buffer.
+            const hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) {
+                rc_ = (int)e;
+                return;
+            }
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        w.pending = false;  // a fresh buffer has no users yet
+        if (hipMalloc(&w.ptr, bytes ? bytes : 8) != hipSuccess) {
+            w.ptr = nullptr;
+            rc_ = ZKIE_ERR_ALLOC;
+            return;
+        }
+        w.bytes = bytes;
+    }
+    if (w.pending) {
+        // Also on the previous lease's own stream: a destroyed stream's handle
+        // can come back for a new stream while the old work still runs.
+        const hipError_t e = hipStreamWaitEvent(s, w.done, 0);
+        if (e != hipSuccess) {
+            rc_ = (int)e;
+            return;
+        }
+    }
+    ptr_ = w.ptr;
+}
+
+Scratch::~Scratch()
+{
+    if (!slot_) return;
+    ScratchSlot& w = *slot_;
+    if (ptr_) {
+        bool recorded = false;
+        if (!w.done) (void)hipEventCreateWithFlags(&w.done, hipEventDisableTiming);
+        if (w.done) recorded = hipEventRecord(w.done, s_) == hipSuccess;
+        // Without an event to order the next lease, wait for this one here.
+        if (!recorded) (void)hipStreamSynchronize(s_);
+        w.pending = recorded;
+    }
+    w.mu.unlock();
 }
 
 ProfMark prof_begin(const char* kernel, hipStream_t s)

@@ -24,11 +24,39 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
         if (zk_e_ != hipSuccess) return (int)zk_e_;    \
     } while (0)
 
-// Grow-only device scratch, one per (device, slot); the same role as the
-// reference's CudaBuffer arenas (cuda_buffer.rs:7-57). Returns nullptr on
-// allocation failure. Not thread-safe across host threads sharing a device.
-enum WorkspaceSlot { WS_NTT = 0, WS_MERKLE = 1, WS_MISC = 2, WS_FOLD = 3, WS_COUNT = 4 };
-void* workspace(WorkspaceSlot slot, size_t bytes);
+// Grow-only device scratch, one buffer per (device, slot); the same role as
+// the reference's CudaBuffer arenas (cuda_buffer.rs:7-57), which the
+// reference serialises behind a Mutex (cuda_buffer.rs:59).
+//
+// A Scratch lease owns its slot from construction to destruction: it holds
+// the slot's host lock while the caller enqueues work that uses the buffer,
+// makes the caller's stream wait for the GPU work of the previous lease (an
+// event recorded when that lease ended, on whatever stream it used), and
+// records its own end on its stream when destroyed. Calls on different
+// streams, or from different host threads, therefore never use one buffer
+// at the same time on the GPU, and none of them blocks the host. Nested
+// leases are taken in the order WS_FOLD, WS_MISC, WS_NTT.
+enum WorkspaceSlot { WS_NTT = 0, WS_MISC = 1, WS_FOLD = 2, WS_COUNT = 3 };
+
+struct ScratchSlot;
+
+class Scratch {
+public:
+    Scratch(WorkspaceSlot slot, size_t bytes, hipStream_t s);
+    ~Scratch();
+    Scratch(const Scratch&) = delete;
+    Scratch& operator=(const Scratch&) = delete;
+    // The buffer (at least `bytes` long), or nullptr when status() != 0.
+    void* get() const { return ptr_; }
+    // 0, a hipError_t, ZKIE_ERR_ALLOC or ZKIE_ERR_NO_DEVICE.
+    int status() const { return rc_; }
+
+private:
+    ScratchSlot* slot_ = nullptr;
+    hipStream_t s_;
+    void* ptr_ = nullptr;
+    int rc_ = 0;
+};
 
 // Kernel timers: when profiling is on, every instrumented launch records a
 // HIP event pair on the launch stream; totals are read back on query.

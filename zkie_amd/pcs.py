@@ -125,7 +125,7 @@ class HipMerkleTreeMmcs:
         rows, sib = self.open_batches([index], tree)
         return rows[0], sib[0]
 
-    def open_batches(self, indices, tree: HipMerkleTree):
+    def open_batches(self, indices, tree: HipMerkleTree, stream=None):
         idx = np.ascontiguousarray(indices, np.uint64)
         n = idx.size
         levels = tree.num_layers() - 1
@@ -133,7 +133,7 @@ class HipMerkleTreeMmcs:
         sib = np.zeros((n, max(levels, 0), 8), np.uint64)
         check(N.load().zkie_merkle_open_batch(
             tree.d_mat.addr, tree.h, tree.w, tree.d_layers.addr, N.p(idx), n,
-            N.p(rows), N.p(sib) if sib.size else ctypes.cast(0, N._u64p), None),
+            N.p(rows), N.p(sib) if sib.size else ctypes.cast(0, N._u64p), stream),
             "zkie_merkle_open_batch")
         return rows, sib
 
