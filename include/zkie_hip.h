@@ -172,6 +172,34 @@ int zkie_fold_rows_at(const uint64_t *d_mat, uint64_t h, uint32_t log_width, int
 int zkie_mle_eval(const uint64_t *d_vals, uint32_t num_vars, int is_ext, const uint64_t *r,
                   uint64_t *out, void *stream);
 
+/* Sumcheck of sum_x f(x) h(x) over tables of 2^num_vars entries, the round
+ * polynomials a WHIR round sends before it folds (compute_sumcheck_polynomials,
+ * p3-whir src/pcs/prover/mod.rs:309-315), with the round and fold rules of
+ * zkIE's sumcheck::prove (crates/zkie-core/src/common/sumcheck.rs:33-89):
+ * entries (2s, 2s+1) pair up (variable 0 is the least-significant index bit),
+ * the round polynomial c0 + c1 X + c2 X^2 interpolates sum_s f(X) h(X) at
+ * X = 0, 1, 2, and binding variable 0 to r maps a table a to
+ * a[2s] + r (a[2s+1] - a[2s]). f is base (f_is_ext = 0) or EF, h is EF, all
+ * EF flattened [c0, c1]; challenges and coefficients are EF.
+ *
+ * zkie_sumcheck_round: the current round's polynomial; poly (host) receives
+ * c0, c1, c2 (6 u64). num_vars >= 1. */
+int zkie_sumcheck_round(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, uint32_t num_vars,
+                        uint64_t *poly, void *stream);
+/* zkie_sumcheck_fold: both tables bound at variable 0 to r (host, one EF);
+ * d_f_out and d_h_out receive 2^(num_vars-1) EF entries each and must not
+ * overlap the inputs or each other. Does not synchronise. */
+int zkie_sumcheck_fold(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, uint32_t num_vars,
+                       const uint64_t *r, uint64_t *d_f_out, uint64_t *d_h_out, void *stream);
+/* zkie_sumcheck_prove: `rounds` rounds with the challenges r (host, rounds EF)
+ * given up front, as sumcheck::prove takes them: polys (host) receives
+ * 6 u64 per round, d_f_out / d_h_out the tables after the last fold
+ * (2^(num_vars-rounds) EF entries each; with rounds = num_vars, f(r) and
+ * h(r)). The outputs must not overlap the inputs or each other. */
+int zkie_sumcheck_prove(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, uint32_t num_vars,
+                        uint32_t rounds, const uint64_t *r, uint64_t *polys, uint64_t *d_f_out,
+                        uint64_t *d_h_out, void *stream);
+
 /* Encoding of commit_extension (p3-whir src/pcs/committer/writer.rs:21-86):
  * the 2^num_vars-entry table (base or EF) as a 2^(num_vars - log_width) x
  * 2^log_width matrix, rows as stored (prefix = 0, VariableOrder::Suffix) or

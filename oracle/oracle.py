@@ -72,6 +72,8 @@ def lib():
             "or_fold_rows": (None, [_u64p, u64, u32, i32, _u64p, _u64p]),
             "or_mle_eval_base": (u64, [_u64p, u32, _u64p]),
             "or_mle_eval": (None, [_u64p, u32, ctypes.c_int, _u64p, _u64p]),
+            "or_sumcheck_prove": (None, [_u64p, ctypes.c_int, _u64p, u32, u32, _u64p, _u64p, _u64p,
+                                         _u64p]),
             "or_xorshift_next": (u64, [_u64p]),
             "or_xorshift_init": (None, [_u64p, u64]),
             "or_gen_uniform": (None, [u64, u64, _u64p]),
@@ -348,6 +350,24 @@ def mle_eval(values, point, is_ext: bool) -> np.ndarray:
     out = np.zeros(2, np.uint64)
     lib().or_mle_eval(_p(v), t, 1 if is_ext else 0, _p(pt), _p(out))
     return out
+
+
+def sumcheck_prove(f, f_is_ext: bool, h, r):
+    """`len(r)` rounds of common/sumcheck.rs:33-89 over sum_x f(x) h(x) with EF
+    tables and challenges. f: 2^t base or flattened EF, h: flattened EF, r:
+    (rounds, 2). Returns (polys (rounds, 3, 2) as c0, c1, c2, f_out, h_out),
+    the folded tables as (2^(t - rounds), 2)."""
+    fv, hv = u64(f).reshape(-1), u64(h).reshape(-1)
+    rr = u64(r).reshape(-1)
+    rounds = rr.size // 2
+    t = (hv.size // 2).bit_length() - 1
+    assert hv.size == 2 << t and fv.size == (2 if f_is_ext else 1) << t and rounds <= t
+    polys = np.zeros((max(rounds, 1), 3, 2), np.uint64)
+    fo = np.zeros((1 << (t - rounds), 2), np.uint64)
+    ho = np.zeros_like(fo)
+    lib().or_sumcheck_prove(_p(fv), 1 if f_is_ext else 0, _p(hv), t, rounds, _p(rr) if rr.size else _p(polys),
+                            _p(polys), _p(fo), _p(ho))
+    return polys[:rounds], fo, ho
 
 
 def whir_encode(poly, num_vars: int, is_ext: bool, log_width: int, log_inv_rate: int,

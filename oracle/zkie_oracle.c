@@ -612,6 +612,61 @@ void or_mle_eval(const uint64_t *values, uint32_t t, int is_ext, const uint64_t 
     free(buf);
 }
 
+/* common/sumcheck.rs:33-89 (prove and fold) with EF tables and challenges. */
+void or_sumcheck_prove(const uint64_t *f, int f_is_ext, const uint64_t *h, uint32_t t, uint32_t rounds,
+                       const uint64_t *r, uint64_t *polys, uint64_t *f_out, uint64_t *h_out)
+{
+    uint64_t n = 1ULL << t;
+    uint64_t *fb = (uint64_t *)malloc(2 * n * sizeof(uint64_t));
+    uint64_t *hb = (uint64_t *)malloc(2 * n * sizeof(uint64_t));
+    for (uint64_t i = 0; i < n; i++) {
+        fb[2 * i] = (f_is_ext ? f[2 * i] : f[i]) % OR_P;
+        fb[2 * i + 1] = f_is_ext ? f[2 * i + 1] % OR_P : 0;
+        hb[2 * i] = h[2 * i] % OR_P;
+        hb[2 * i + 1] = h[2 * i + 1] % OR_P;
+    }
+    const uint64_t inv2 = OR_P / 2 + 1;
+    for (uint32_t i = 0; i < rounds; i++) {
+        const uint64_t half = n / 2;
+        uint64_t y0[2] = {0, 0}, y1[2] = {0, 0}, y2[2] = {0, 0};
+        for (uint64_t s2 = 0; s2 < half; s2++) {
+            const uint64_t *f0 = fb + 4 * s2, *f1 = fb + 4 * s2 + 2;
+            const uint64_t *h0 = hb + 4 * s2, *h1 = hb + 4 * s2 + 2;
+            uint64_t f2[2], h2[2], m[2];
+            f2[0] = or_sub(or_add(f1[0], f1[0]), f0[0]);
+            f2[1] = or_sub(or_add(f1[1], f1[1]), f0[1]);
+            h2[0] = or_sub(or_add(h1[0], h1[0]), h0[0]);
+            h2[1] = or_sub(or_add(h1[1], h1[1]), h0[1]);
+            or_ef_mul(f0, h0, m);
+            ef_add(y0, m, y0);
+            or_ef_mul(f1, h1, m);
+            ef_add(y1, m, y1);
+            or_ef_mul(f2, h2, m);
+            ef_add(y2, m, y2);
+        }
+        uint64_t *c = polys + 6 * i;
+        for (int e = 0; e < 2; e++) {
+            c[e] = y0[e];
+            c[2 + e] = or_mul(or_sub(or_sub(or_mul(4, y1[e]), y2[e]), or_mul(3, y0[e])), inv2);
+            c[4 + e] = or_mul(or_add(or_sub(y2[e], or_mul(2, y1[e])), y0[e]), inv2);
+        }
+        for (uint64_t s2 = 0; s2 < half; s2++) {
+            uint64_t d[2], m[2];
+            ef_sub(fb + 4 * s2 + 2, fb + 4 * s2, d);
+            or_ef_mul(r + 2 * i, d, m);
+            ef_add(fb + 4 * s2, m, fb + 2 * s2);
+            ef_sub(hb + 4 * s2 + 2, hb + 4 * s2, d);
+            or_ef_mul(r + 2 * i, d, m);
+            ef_add(hb + 4 * s2, m, hb + 2 * s2);
+        }
+        n = half;
+    }
+    memcpy(f_out, fb, 2 * n * sizeof(uint64_t));
+    memcpy(h_out, hb, 2 * n * sizeof(uint64_t));
+    free(fb);
+    free(hb);
+}
+
 void or_fold_rows(const uint64_t *mat, uint64_t h, uint32_t k, int is_ext, const uint64_t *r,
                   uint64_t *out)
 {

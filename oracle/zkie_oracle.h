@@ -115,6 +115,17 @@ uint64_t or_mle_eval_base(const uint64_t *values, uint32_t t, const uint64_t *po
  * the out-of-domain answer of a WHIR round. out: one EF element. */
 void or_mle_eval(const uint64_t *values, uint32_t t, int is_ext, const uint64_t *point, uint64_t out[2]);
 
+/* ---- sumcheck of a product of two multilinear tables (common/sumcheck.rs:33-89) ---- */
+/* `rounds` rounds of sumcheck::prove over sum_x f(x) h(x), 2^t entries, f base
+ * (f_is_ext = 0) or EF, h EF (flattened [c0, c1]), challenges r (rounds EF).
+ * Round i pairs entries (2s, 2s+1) (variable 0 = the least-significant index
+ * bit), sums y_X = sum_s f(X) h(X) at X = 0, 1, 2 (f(2) = 2 f1 - f0), writes
+ * c0 = y0, c1 = (4 y1 - y2 - 3 y0) / 2, c2 = (y2 - 2 y1 + y0) / 2 as 3 EF to
+ * polys + 6i, then folds both tables, b[i] = a0 + r (a1 - a0). f_out and h_out
+ * receive the folded EF tables (2^(t-rounds) entries each). */
+void or_sumcheck_prove(const uint64_t *f, int f_is_ext, const uint64_t *h, uint32_t t, uint32_t rounds,
+                       const uint64_t *r, uint64_t *polys, uint64_t *f_out, uint64_t *h_out);
+
 /* ---- inputs (field.rs:17-36, fixed_point.rs:11-38) ---- */
 uint64_t or_xorshift_next(uint64_t *state);
 void or_xorshift_init(uint64_t *state, uint64_t seed);

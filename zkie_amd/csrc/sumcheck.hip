@@ -1,0 +1,284 @@
+// Sumcheck rounds of a product of two multilinear tables on MI355X: the
+// round polynomials the WHIR prover sends before each fold
+// (compute_sumcheck_polynomials, p3-whir src/pcs/prover/mod.rs:309-315),
+// with the round and fold rules of zkIE's own sumcheck::prove
+// (crates/zkie-core/src/common/sumcheck.rs:33-89):
+//   round: pair the entries (2s, 2s + 1) (variable 0 = the least-significant
+//          index bit), y_X = sum_s f(X) h(X) at X = 0, 1, 2 with
+//          f(2) = 2 f1 - f0; c0 = y0, c1 = (4 y1 - y2 - 3 y0) / 2,
+//          c2 = (y2 - 2 y1 + y0) / 2;
+//   fold:  b[s] = a[2s] + r (a[2s + 1] - a[2s]) for both tables.
+// f is base or EF, h and every folded table EF = F[x]/(x^2 - 7) flattened
+// [c0, c1]; challenges are EF. Both kernels stream their tables once
+// (HBM-bound): the round kernel reduces its three EF sums per workgroup in
+// LDS and one small workgroup adds the partial sums.
+#include <vector>
+
+#include "gl64.hpp"
+#include "runtime.hpp"
+
+namespace zk {
+namespace {
+
+constexpr int kScThreads = 256;
+constexpr uint32_t kScMaxBlocks = 2048;  // workgroups of a round kernel (partial sums)
+
+template <bool FEXT>
+__device__ __forceinline__ Ef sc_load_f(const uint64_t* __restrict__ f, uint64_t i)
+{
+    if constexpr (FEXT)
+        return Ef{f[2 * i], f[2 * i + 1]};
+    else
+        return Ef{f[i], 0};
+}
+
+template <bool FEXT>
+__device__ __forceinline__ Ef sc_mul(Ef f, Ef h)
+{
+    if constexpr (FEXT)
+        return ef_mul(f, h);
+    else
+        return ef_mul_base(h, f.c0);
+}
+
+// Six u64 per thread reduced over the workgroup; thread 0 gets the sums.
+__device__ __forceinline__ void sc_block_reduce(uint64_t v[6], uint64_t (*red)[kScThreads])
+{
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < 6; e++) red[e][tid] = v[e];
+    __syncthreads();
+#pragma unroll 1
+    for (uint32_t w = kScThreads / 2; w > 0; w >>= 1) {
+        if (tid < w) {
+#pragma unroll
+            for (int e = 0; e < 6; e++) red[e][tid] = gl_add(red[e][tid], red[e][tid + w]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int e = 0; e < 6; e++) v[e] = red[e][0];
+}
+
+// Partial sums [y0, y1, y2] (EF each) of the pairs s = gid, gid + stride, ...
+// below `half`; one record of 6 u64 per workgroup.
+template <bool FEXT>
+__global__ __launch_bounds__(kScThreads) void sc_round_kernel(const uint64_t* __restrict__ f,
+                                                              const uint64_t* __restrict__ h, uint64_t half,
+                                                              uint64_t* __restrict__ partial)
+{
+    __shared__ uint64_t red[6][kScThreads];
+    Ef y0{0, 0}, y1{0, 0}, y2{0, 0};
+    const uint64_t stride = (uint64_t)gridDim.x * kScThreads;
+    for (uint64_t s = (uint64_t)blockIdx.x * kScThreads + threadIdx.x; s < half; s += stride) {
+        const Ef f0 = sc_load_f<FEXT>(f, 2 * s), f1 = sc_load_f<FEXT>(f, 2 * s + 1);
+        const Ef h0{h[4 * s], h[4 * s + 1]}, h1{h[4 * s + 2], h[4 * s + 3]};
+        const Ef f2 = ef_sub(ef_add(f1, f1), f0), h2 = ef_sub(ef_add(h1, h1), h0);
+        y0 = ef_add(y0, sc_mul<FEXT>(f0, h0));
+        y1 = ef_add(y1, sc_mul<FEXT>(f1, h1));
+        y2 = ef_add(y2, sc_mul<FEXT>(f2, h2));
+    }
+    uint64_t v[6] = {y0.c0, y0.c1, y1.c0, y1.c1, y2.c0, y2.c1};
+    sc_block_reduce(v, red);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int e = 0; e < 6; e++) partial[6 * (uint64_t)blockIdx.x + e] = gl_canon(v[e]);
+    }
+}
+
+// One workgroup: the sum of `nblocks` partial records into out[0..6).
+__global__ __launch_bounds__(kScThreads) void sc_finish_kernel(const uint64_t* __restrict__ partial,
+                                                               uint32_t nblocks, uint64_t* __restrict__ out)
+{
+    __shared__ uint64_t red[6][kScThreads];
+    uint64_t v[6] = {0, 0, 0, 0, 0, 0};
+    for (uint32_t b = threadIdx.x; b < nblocks; b += kScThreads) {
+#pragma unroll
+        for (int e = 0; e < 6; e++) v[e] = gl_add(v[e], partial[6 * (uint64_t)b + e]);
+    }
+    sc_block_reduce(v, red);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int e = 0; e < 6; e++) out[e] = gl_canon(v[e]);
+    }
+}
+
+// Both tables bound at variable 0: out[s] = a[2s] + r (a[2s + 1] - a[2s]),
+// s < half, outputs EF.
+template <bool FEXT>
+__global__ __launch_bounds__(kScThreads) void sc_fold_kernel(const uint64_t* __restrict__ f,
+                                                             const uint64_t* __restrict__ h, uint64_t half,
+                                                             uint64_t r0, uint64_t r1,
+                                                             uint64_t* __restrict__ f_out,
+                                                             uint64_t* __restrict__ h_out)
+{
+    const uint64_t s = (uint64_t)blockIdx.x * kScThreads + threadIdx.x;
+    if (s >= half) return;
+    const Ef r{r0, r1};
+    const Ef f0 = sc_load_f<FEXT>(f, 2 * s), f1 = sc_load_f<FEXT>(f, 2 * s + 1);
+    const Ef h0{h[4 * s], h[4 * s + 1]}, h1{h[4 * s + 2], h[4 * s + 3]};
+    const Ef fo = ef_add(f0, ef_mul(r, ef_sub(f1, f0)));
+    const Ef ho = ef_add(h0, ef_mul(r, ef_sub(h1, h0)));
+    f_out[2 * s] = gl_canon(fo.c0);
+    f_out[2 * s + 1] = gl_canon(fo.c1);
+    h_out[2 * s] = gl_canon(ho.c0);
+    h_out[2 * s + 1] = gl_canon(ho.c1);
+}
+
+// Round sums of tables of 2^m entries (m >= 1) into d_sums (6 u64), using
+// `partial` (kScMaxBlocks records of 6 u64).
+int sc_sums(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, uint64_t* partial,
+            uint64_t* d_sums, hipStream_t s)
+{
+    const uint64_t half = 1ull << (m - 1);
+    const uint64_t want = (half + kScThreads - 1) / kScThreads;
+    const uint32_t blocks = (uint32_t)(want < kScMaxBlocks ? want : kScMaxBlocks);
+    ProfMark pm = prof_begin("sumcheck_round", s);
+    if (f_ext)
+        sc_round_kernel<true><<<blocks, kScThreads, 0, s>>>(d_f, d_h, half, partial);
+    else
+        sc_round_kernel<false><<<blocks, kScThreads, 0, s>>>(d_f, d_h, half, partial);
+    ZK_LAUNCHED();
+    sc_finish_kernel<<<1, kScThreads, 0, s>>>(partial, blocks, d_sums);
+    prof_end(pm, s);
+    ZK_LAUNCHED();
+    return ZKIE_OK;
+}
+
+// c0, c1, c2 (EF each, canonical) from y0, y1, y2 (sumcheck.rs:65-67).
+void sc_coefficients(const uint64_t y[6], uint64_t poly[6])
+{
+    for (int e = 0; e < 2; e++) {
+        const uint64_t y0 = y[e], y1 = y[2 + e], y2 = y[4 + e];
+        const uint64_t c1 = gl_halve(gl_sub(gl_sub(gl_mul(4, y1), y2), gl_mul(3, y0)));
+        const uint64_t c2 = gl_halve(gl_add(gl_sub(y2, gl_add(y1, y1)), y0));
+        poly[e] = gl_canon(y0);
+        poly[2 + e] = gl_canon(c1);
+        poly[4 + e] = gl_canon(c2);
+    }
+}
+
+int sc_fold(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, const uint64_t* r,
+            uint64_t* d_f_out, uint64_t* d_h_out, hipStream_t s)
+{
+    const uint64_t half = 1ull << (m - 1);
+    const uint64_t blocks = (half + kScThreads - 1) / kScThreads;
+    const uint64_t r0 = gl_canon(r[0]), r1 = gl_canon(r[1]);
+    ProfMark pm = prof_begin("sumcheck_fold", s);
+    if (f_ext)
+        sc_fold_kernel<true><<<(unsigned)blocks, kScThreads, 0, s>>>(d_f, d_h, half, r0, r1, d_f_out, d_h_out);
+    else
+        sc_fold_kernel<false><<<(unsigned)blocks, kScThreads, 0, s>>>(d_f, d_h, half, r0, r1, d_f_out, d_h_out);
+    prof_end(pm, s);
+    ZK_LAUNCHED();
+    return ZKIE_OK;
+}
+
+// [a, a + n) and [b, b + m) (u64 counts) share memory.
+bool overlaps(const uint64_t* a, uint64_t n, const uint64_t* b, uint64_t m) { return a < b + m && b < a + n; }
+
+}  // namespace
+}  // namespace zk
+
+using namespace zk;
+
+extern "C" {
+
+int zkie_sumcheck_round(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, uint32_t num_vars,
+                        uint64_t* poly, void* stream)
+{
+    if (num_vars < 1 || num_vars > 34 || !d_f || !d_h || !poly) return ZKIE_ERR_INVALID;
+    hipStream_t s = as_stream(stream);
+    Scratch ws(WS_MISC, (kScMaxBlocks + 1) * 6 * 8, s);
+    if (ws.status()) return ws.status();
+    uint64_t* partial = (uint64_t*)ws.get();
+    uint64_t* d_sums = partial + 6 * kScMaxBlocks;
+    int rc = sc_sums(d_f, f_is_ext != 0, d_h, num_vars, partial, d_sums, s);
+    if (rc) return rc;
+    uint64_t y[6];
+    ZK_TRY(hipMemcpyAsync(y, d_sums, sizeof(y), hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    sc_coefficients(y, poly);
+    return ZKIE_OK;
+}
+
+int zkie_sumcheck_fold(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, uint32_t num_vars,
+                       const uint64_t* r, uint64_t* d_f_out, uint64_t* d_h_out, void* stream)
+{
+    if (num_vars < 1 || num_vars > 34 || !d_f || !d_h || !r || !d_f_out || !d_h_out) return ZKIE_ERR_INVALID;
+    const uint64_t n = 1ull << num_vars, half = n >> 1;
+    const uint64_t nf = f_is_ext ? 2 * n : n;
+    if (overlaps(d_f_out, 2 * half, d_f, nf) || overlaps(d_f_out, 2 * half, d_h, 2 * n) ||
+        overlaps(d_h_out, 2 * half, d_f, nf) || overlaps(d_h_out, 2 * half, d_h, 2 * n) ||
+        overlaps(d_f_out, 2 * half, d_h_out, 2 * half))
+        return ZKIE_ERR_INVALID;
+    return sc_fold(d_f, f_is_ext != 0, d_h, num_vars, r, d_f_out, d_h_out, as_stream(stream));
+}
+
+int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, uint32_t num_vars,
+                        uint32_t rounds, const uint64_t* r, uint64_t* polys, uint64_t* d_f_out,
+                        uint64_t* d_h_out, void* stream)
+{
+    if (num_vars > 34 || rounds > num_vars || !d_f || !d_h || !d_f_out || !d_h_out ||
+        (rounds && (!r || !polys)))
+        return ZKIE_ERR_INVALID;
+    hipStream_t s = as_stream(stream);
+    const uint64_t n = 1ull << num_vars, nout = n >> rounds;
+    const uint64_t nf = f_is_ext ? 2 * n : n;
+    if (overlaps(d_f_out, 2 * nout, d_f, nf) || overlaps(d_f_out, 2 * nout, d_h, 2 * n) ||
+        overlaps(d_h_out, 2 * nout, d_f, nf) || overlaps(d_h_out, 2 * nout, d_h, 2 * n) ||
+        overlaps(d_f_out, 2 * nout, d_h_out, 2 * nout))
+        return ZKIE_ERR_INVALID;
+    if (rounds == 0) {
+        // no round: the tables themselves, f lifted to EF
+        if (f_is_ext) {
+            ZK_TRY(hipMemcpyAsync(d_f_out, d_f, 16 * n, hipMemcpyDeviceToDevice, s));
+        } else {
+            ZK_TRY(hipMemsetAsync(d_f_out, 0, 16 * n, s));
+            ZK_TRY(hipMemcpy2DAsync(d_f_out, 16, d_f, 8, 8, n, hipMemcpyDeviceToDevice, s));
+        }
+        ZK_TRY(hipMemcpyAsync(d_h_out, d_h, 16 * n, hipMemcpyDeviceToDevice, s));
+        return ZKIE_OK;
+    }
+    // Workspace: partial sums, then every round's y sums (6 u64 each), then
+    // the folded tables of the intermediate rounds: even rounds write region
+    // A (f, h of at most `half` EF entries each: 4 half u64), odd rounds region
+    // B after it (at most half / 2 entries each: 2 half u64).
+    const uint64_t half = n >> 1;
+    const uint64_t pool_u64 = rounds > 1 ? 6 * half : 0;
+    Scratch ws(WS_FOLD, (6 * (kScMaxBlocks + rounds) + pool_u64) * 8, s);
+    if (ws.status()) return ws.status();
+    uint64_t* partial = (uint64_t*)ws.get();
+    uint64_t* d_y = partial + 6 * kScMaxBlocks;
+    uint64_t* pool = d_y + 6 * rounds;
+    const uint64_t* cf = d_f;
+    const uint64_t* ch = d_h;
+    bool ext = f_is_ext != 0;
+    for (uint32_t i = 0; i < rounds; i++) {
+        const uint32_t m = num_vars - i;
+        int rc = sc_sums(cf, ext, ch, m, partial, d_y + 6 * i, s);
+        if (rc) return rc;
+        uint64_t *nf_, *nh_;
+        if (i + 1 == rounds) {
+            nf_ = d_f_out;
+            nh_ = d_h_out;
+        } else {
+            // round i writes half >> i EF entries per table
+            uint64_t* base = (i % 2 == 0) ? pool : pool + 4 * half;
+            nf_ = base;
+            nh_ = base + (i % 2 == 0 ? 2 * half : half);
+        }
+        rc = sc_fold(cf, ext, ch, m, r + 2 * i, nf_, nh_, s);
+        if (rc) return rc;
+        cf = nf_;
+        ch = nh_;
+        ext = true;
+    }
+    std::vector<uint64_t> y(6 * rounds);
+    ZK_TRY(hipMemcpyAsync(y.data(), d_y, y.size() * 8, hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    for (uint32_t i = 0; i < rounds; i++) sc_coefficients(y.data() + 6 * i, polys + 6 * i);
+    return ZKIE_OK;
+}
+
+}  // extern "C"

@@ -212,6 +212,44 @@ def fold_rows_at(d_mat: DeviceBuffer, h: int, k: int, is_ext: bool, indices, r, 
     return out.reshape(-1, 2)
 
 
+def sumcheck_round(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int,
+                   stream=None) -> np.ndarray:
+    """The current round polynomial of the sumcheck of sum_x f(x) h(x)
+    (common/sumcheck.rs:47-68): c0, c1, c2 as a (3, 2) EF array."""
+    poly = np.zeros((3, 2), np.uint64)
+    check(N.load().zkie_sumcheck_round(d_f.addr, 1 if f_is_ext else 0, d_h.addr, num_vars, N.p(poly), stream),
+          "zkie_sumcheck_round")
+    return poly
+
+
+def sumcheck_fold(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int, r,
+                  stream=None) -> tuple[DeviceBuffer, DeviceBuffer]:
+    """Both tables bound at variable 0 to the EF challenge r
+    (common/sumcheck.rs:81-89); returns the two folded EF tables."""
+    rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
+    assert rr.size == 2
+    half = 1 << (num_vars - 1)
+    f_out, h_out = DeviceBuffer(2 * half), DeviceBuffer(2 * half)
+    check(N.load().zkie_sumcheck_fold(d_f.addr, 1 if f_is_ext else 0, d_h.addr, num_vars, N.p(rr),
+                                      f_out.addr, h_out.addr, stream), "zkie_sumcheck_fold")
+    return f_out, h_out
+
+
+def sumcheck_prove(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int, r,
+                   stream=None) -> tuple[np.ndarray, DeviceBuffer, DeviceBuffer]:
+    """len(r) rounds of sumcheck::prove (common/sumcheck.rs:33-79) with the
+    challenges given up front: (polys (rounds, 3, 2), f_out, h_out)."""
+    rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
+    rounds = rr.size // 2
+    polys = np.zeros((max(rounds, 1), 3, 2), np.uint64)
+    n_out = 1 << (num_vars - rounds)
+    f_out, h_out = DeviceBuffer(2 * n_out), DeviceBuffer(2 * n_out)
+    check(N.load().zkie_sumcheck_prove(d_f.addr, 1 if f_is_ext else 0, d_h.addr, num_vars, rounds,
+                                       N.p(rr) if rr.size else N.p(polys), N.p(polys), f_out.addr,
+                                       h_out.addr, stream), "zkie_sumcheck_prove")
+    return polys[:rounds], f_out, h_out
+
+
 def mle_eval(d_vals: DeviceBuffer, num_vars: int, is_ext: bool, r, stream=None) -> np.ndarray:
     """sum_j eq(r, j) v[j] over a device table of 2^num_vars entries (EF, host)."""
     rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
