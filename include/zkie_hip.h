@@ -191,6 +191,11 @@ int zkie_sumcheck_round(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, 
  * overlap the inputs or each other. Does not synchronise. */
 int zkie_sumcheck_fold(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, uint32_t num_vars,
                        const uint64_t *r, uint64_t *d_f_out, uint64_t *d_h_out, void *stream);
+/* zkie_eq_table: the weight table of one evaluation constraint,
+ * d_out[x] = eq(point, x) = prod_b (x_b ? p_b : 1 - p_b) for x < 2^num_vars
+ * (EF, bit 0 of x first, mle.rs:44-56), so that sum_x eq(p, x) f(x) = f(p)
+ * (mle.rs:8-22). point (host): num_vars EF coordinates. */
+int zkie_eq_table(const uint64_t *point, uint32_t num_vars, uint64_t *d_out, void *stream);
 /* zkie_sumcheck_prove: `rounds` rounds with the challenges r (host, rounds EF)
  * given up front, as sumcheck::prove takes them: polys (host) receives
  * 6 u64 per round, d_f_out / d_h_out the tables after the last fold

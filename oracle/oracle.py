@@ -72,6 +72,7 @@ def lib():
             "or_fold_rows": (None, [_u64p, u64, u32, i32, _u64p, _u64p]),
             "or_mle_eval_base": (u64, [_u64p, u32, _u64p]),
             "or_mle_eval": (None, [_u64p, u32, ctypes.c_int, _u64p, _u64p]),
+            "or_eq_table": (None, [_u64p, u32, _u64p]),
             "or_sumcheck_prove": (None, [_u64p, ctypes.c_int, _u64p, u32, u32, _u64p, _u64p, _u64p,
                                          _u64p]),
             "or_xorshift_next": (u64, [_u64p]),
@@ -349,6 +350,15 @@ def mle_eval(values, point, is_ext: bool) -> np.ndarray:
     assert v.size == (2 if is_ext else 1) << t
     out = np.zeros(2, np.uint64)
     lib().or_mle_eval(_p(v), t, 1 if is_ext else 0, _p(pt), _p(out))
+    return out
+
+
+def eq_table(point) -> np.ndarray:
+    """eq(point, x) for x < 2^t, bit 0 first (mle.rs:44-56): (2^t, 2) EF."""
+    pt = u64(point).reshape(-1)
+    t = pt.size // 2
+    out = np.zeros((1 << t, 2), np.uint64)
+    lib().or_eq_table(_p(pt) if pt.size else _p(out), t, _p(out))
     return out
 
 

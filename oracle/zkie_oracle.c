@@ -612,6 +612,24 @@ void or_mle_eval(const uint64_t *values, uint32_t t, int is_ext, const uint64_t 
     free(buf);
 }
 
+/* mle.rs:44-56 (eq_evals), coordinate b doubling the table: entries with bit b
+ * set take p_b, the others 1 - p_b. */
+void or_eq_table(const uint64_t *point, uint32_t t, uint64_t *out)
+{
+    out[0] = 1;
+    out[1] = 0;
+    for (uint32_t b = 0; b < t; b++) {
+        const uint64_t m = 1ULL << b;
+        const uint64_t z[2] = {point[2 * b] % OR_P, point[2 * b + 1] % OR_P};
+        const uint64_t om[2] = {or_sub(1, z[0]), or_sub(0, z[1])};
+        for (uint64_t j = 0; j < m; j++) {
+            uint64_t v[2] = {out[2 * j], out[2 * j + 1]};
+            or_ef_mul(v, z, out + 2 * (j + m));
+            or_ef_mul(v, om, out + 2 * j);
+        }
+    }
+}
+
 /* common/sumcheck.rs:33-89 (prove and fold) with EF tables and challenges. */
 void or_sumcheck_prove(const uint64_t *f, int f_is_ext, const uint64_t *h, uint32_t t, uint32_t rounds,
                        const uint64_t *r, uint64_t *polys, uint64_t *f_out, uint64_t *h_out)

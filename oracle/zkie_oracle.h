@@ -126,6 +126,10 @@ void or_mle_eval(const uint64_t *values, uint32_t t, int is_ext, const uint64_t 
 void or_sumcheck_prove(const uint64_t *f, int f_is_ext, const uint64_t *h, uint32_t t, uint32_t rounds,
                        const uint64_t *r, uint64_t *polys, uint64_t *f_out, uint64_t *h_out);
 
+/* eq(p, x) = prod_b (x_b ? p_b : 1 - p_b) for x < 2^t, bit 0 first (mle.rs:44-56),
+ * EF point (t coordinates), out: 2^t EF entries. */
+void or_eq_table(const uint64_t *point, uint32_t t, uint64_t *out);
+
 /* ---- inputs (field.rs:17-36, fixed_point.rs:11-38) ---- */
 uint64_t or_xorshift_next(uint64_t *state);
 void or_xorshift_init(uint64_t *state, uint64_t seed);

@@ -161,6 +161,13 @@ def test_whir_rounds_ood_and_stir_full_size(native, oracle):
         n_vars = t_entries.bit_length() - 1
         for z, ans in zip(rnd.ood_points, rnd.ood_answers):
             assert (ans == oracle.mle_eval(tab, C.ef_pow2_chain(z, n_vars), True)).all()
+        # the sumcheck rounds that folded the previous table (its weight: the
+        # eq table of the round's evaluation constraint)
+        ch = C.challenges(k * wl.rounds)[k * (r - 1):k * r]
+        prev_tab = (PL.workload_inputs(wl).reshape(-1) if r == 1 else out.tables[r - 2][0].download())
+        polys, f_out, _ = oracle.sumcheck_prove(prev_tab, r > 1, oracle.eq_table(rnd.weight_point), ch)
+        assert (rnd.sumcheck_polys == polys).all()
+        assert (tab.reshape(-1, 2) == f_out).all()
         idx = rnd.stir_indices.astype(np.int64)
         prev_cw = prev.codeword.download().reshape(prev.rows, prev.width)
         ch = C.challenges(k * wl.rounds)[k * (r - 1):k * r]

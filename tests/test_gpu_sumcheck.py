@@ -87,3 +87,12 @@ def test_rejects_overlap_and_bad_sizes(native, oracle):
     rs = np.ascontiguousarray(r.reshape(-1))
     assert L.zkie_sumcheck_prove(d_f.addr, 1, d_h.addr, t, t + 1, p(rs), p(polys), out.addr,
                                  out.addr + 2, None) == -1
+
+
+@pytest.mark.parametrize("t", [0, 1, 2, 7, 16, 22])
+def test_eq_table_matches_oracle(native, oracle, t):
+    from zkie_amd import pcs
+
+    print(f"CASE eq_table t={t}", flush=True)
+    pt = (oracle.gen_uniform(1500 + t, 2 * t) % np.uint64(P)).reshape(t, 2)
+    assert (pcs.eq_table(pt).download().reshape(-1, 2) == oracle.eq_table(pt)).all()

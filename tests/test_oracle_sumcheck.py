@@ -145,3 +145,32 @@ def test_rounds_leave_the_table_fold(oracle, t, k, f_ext):
     E = 2 if f_ext else 1
     assert (fo == oracle.fold_rows(f.reshape(-1, E << k), k, r[:k], f_ext)).all()
     assert (ho == oracle.fold_rows(h.reshape(-1, 2 << k), k, r[:k], True)).all()
+
+
+@pytest.mark.parametrize("t", [0, 1, 3, 7])
+def test_eq_table_is_the_product_formula(oracle, t):
+    """Each entry against the product over its bits, written per entry
+    (mle.rs:44-56 states the same table by doubling)."""
+    pt = (oracle.gen_uniform(130 + t, 2 * t) % np.uint64(P)).reshape(t, 2)
+    got = oracle.eq_table(pt)
+    for x in range(1 << t):
+        e = (1, 0)
+        for b in range(t):
+            z = (int(pt[b][0]), int(pt[b][1]))
+            e = ef_mul(e, z if (x >> b) & 1 else ((1 - z[0]) % P, (-z[1]) % P))
+        assert (int(got[x][0]), int(got[x][1])) == e
+
+
+@pytest.mark.parametrize("f_ext", [False, True])
+@pytest.mark.parametrize("t", [1, 6, 10])
+def test_eq_table_weights_evaluate(oracle, t, f_ext):
+    """sum_x eq(p, x) f(x) = f(p), the multilinear evaluation (mle.rs:8-22)."""
+    pt = (oracle.gen_uniform(140 + t, 2 * t) % np.uint64(P)).reshape(t, 2)
+    f = oracle.gen_uniform(150 + t, (2 if f_ext else 1) << t)
+    fv = f.reshape(-1, 2) if f_ext else np.stack([f, np.zeros_like(f)], 1)
+    eq = oracle.eq_table(pt)
+    s = (0, 0)
+    for a, b in zip(eq, fv):
+        s = ef_add(s, ef_mul((int(a[0]), int(a[1])), (int(b[0]) % P, int(b[1]) % P)))
+    want = oracle.mle_eval(f, pt, f_ext)
+    assert s == (int(want[0]), int(want[1]))

@@ -23,7 +23,7 @@ from dataclasses import dataclass
 import numpy as np
 
 GEN_UNIFORM, GEN_I16, GEN_I8, GEN_GAUSS_I16 = 0, 1, 2, 3
-SEED_DATA, SEED_CHALLENGES, SEED_QUERIES, SEED_OOD = 0, 1, 2, 3
+SEED_DATA, SEED_CHALLENGES, SEED_QUERIES, SEED_OOD, SEED_WEIGHTS = 0, 1, 2, 3, 4
 P = 0xFFFFFFFF00000001
 
 

@@ -174,6 +174,40 @@ int sc_fold(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, co
     return ZKIE_OK;
 }
 
+// eq(p, x) = prod_b (x_b ? p_b : 1 - p_b) for x < 2^n (bit 0 first):
+// lo[x mod 2^L] * hi[x >> L], both halves formed on the host.
+__global__ __launch_bounds__(kScThreads) void sc_eq_kernel(const uint64_t* __restrict__ lo,
+                                                           const uint64_t* __restrict__ hi, uint32_t L,
+                                                           uint64_t n, uint64_t* __restrict__ out)
+{
+    const uint64_t x = (uint64_t)blockIdx.x * kScThreads + threadIdx.x;
+    if (x >= n) return;
+    const uint64_t a = x & ((1ull << L) - 1), b = x >> L;
+    const Ef e = ef_mul(Ef{lo[2 * a], lo[2 * a + 1]}, Ef{hi[2 * b], hi[2 * b + 1]});
+    out[2 * x] = gl_canon(e.c0);
+    out[2 * x + 1] = gl_canon(e.c1);
+}
+
+// eq table of the coordinates p[0..k) (EF) into out (2^k EF, host).
+void eq_half_table(const uint64_t* p, uint32_t k, uint64_t* out)
+{
+    out[0] = 1;
+    out[1] = 0;
+    for (uint32_t b = 0; b < k; b++) {
+        const uint64_t m = 1ull << b;
+        const Ef z{gl_canon(p[2 * b]), gl_canon(p[2 * b + 1])};
+        const Ef one_minus{gl_sub(1, z.c0), gl_neg(z.c1)};
+        for (uint64_t j = 0; j < m; j++) {
+            const Ef v{out[2 * j], out[2 * j + 1]};
+            const Ef v1 = ef_mul(v, z), v0 = ef_mul(v, one_minus);
+            out[2 * (j + m)] = gl_canon(v1.c0);
+            out[2 * (j + m) + 1] = gl_canon(v1.c1);
+            out[2 * j] = gl_canon(v0.c0);
+            out[2 * j + 1] = gl_canon(v0.c1);
+        }
+    }
+}
+
 // [a, a + n) and [b, b + m) (u64 counts) share memory.
 bool overlaps(const uint64_t* a, uint64_t n, const uint64_t* b, uint64_t m) { return a < b + m && b < a + n; }
 
@@ -213,6 +247,26 @@ int zkie_sumcheck_fold(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, u
         overlaps(d_f_out, 2 * half, d_h_out, 2 * half))
         return ZKIE_ERR_INVALID;
     return sc_fold(d_f, f_is_ext != 0, d_h, num_vars, r, d_f_out, d_h_out, as_stream(stream));
+}
+
+int zkie_eq_table(const uint64_t* point, uint32_t num_vars, uint64_t* d_out, void* stream)
+{
+    if (num_vars > 34 || !d_out || (num_vars && !point)) return ZKIE_ERR_INVALID;
+    hipStream_t s = as_stream(stream);
+    const uint32_t L = (num_vars + 1) / 2, Hb = num_vars - L;
+    std::vector<uint64_t> tabs(2 * ((1ull << L) + (1ull << Hb)));
+    eq_half_table(point, L, tabs.data());
+    eq_half_table(point + 2 * L, Hb, tabs.data() + 2 * (1ull << L));
+    Scratch ws(WS_MISC, tabs.size() * 8, s);
+    if (ws.status()) return ws.status();
+    uint64_t* d_tabs = (uint64_t*)ws.get();
+    ZK_TRY(hipMemcpyAsync(d_tabs, tabs.data(), tabs.size() * 8, hipMemcpyHostToDevice, s));
+    const uint64_t n = 1ull << num_vars;
+    sc_eq_kernel<<<(unsigned)((n + kScThreads - 1) / kScThreads), kScThreads, 0, s>>>(
+        d_tabs, d_tabs + 2 * (1ull << L), L, n, d_out);
+    ZK_LAUNCHED();
+    ZK_TRY(hipStreamSynchronize(s));  // the halves were copied from a host vector
+    return ZKIE_OK;
 }
 
 int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, uint32_t num_vars,

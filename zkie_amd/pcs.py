@@ -222,6 +222,17 @@ def sumcheck_round(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_var
     return poly
 
 
+def eq_table(point, stream=None) -> DeviceBuffer:
+    """eq(point, x) for every x < 2^n (EF, bit 0 first; mle.rs:44-56) as a
+    device table: the weight table of one evaluation constraint."""
+    pt = np.ascontiguousarray(np.asarray(point, np.uint64).reshape(-1))
+    n = pt.size // 2
+    out = DeviceBuffer(2 << n)
+    check(N.load().zkie_eq_table(N.p(pt) if pt.size else N.p(np.zeros(2, np.uint64)), n, out.addr, stream),
+          "zkie_eq_table")
+    return out
+
+
 def sumcheck_fold(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int, r,
                   stream=None) -> tuple[DeviceBuffer, DeviceBuffer]:
     """Both tables bound at variable 0 to the EF challenge r

@@ -7,8 +7,12 @@ commit_round  <- one WHIR round's encode + commit: p3-whir
 fold          <- the row fold of p3-whir src/pcs/prover/mod.rs:257-290 and the
                  table fold over the low k variables (common/mle.rs:25-38)
 round loop    <- WhirProver::round (prover/mod.rs:196-300) with seeded
-                 challenges: fold the table, encode + commit it, answer
-                 out-of-domain samples on the new table (mod.rs:226-236), then
+                 challenges: k sumcheck rounds over the table times the
+                 weight table of one seeded evaluation constraint
+                 (compute_sumcheck_polynomials, mod.rs:309-315, with the rules
+                 of common/sumcheck.rs:33-89), which leave the table folded
+                 over its low k variables; encode + commit the folded table,
+                 answer out-of-domain samples on it (mod.rs:226-236), then
                  open the previous codeword at STIR indices and fold the opened
                  rows with the round's challenges (mod.rs:247-290)
 run_workload  <- the five workloads of zkie_amd.configs, everything in HBM;
@@ -21,10 +25,10 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _native as N
-from .configs import (SEED_CHALLENGES, SEED_DATA, SEED_OOD, SEED_QUERIES, Workload, XorShift64,
-                      challenges, ef_pow2_chain, query_indices)
-from .pcs import (HipMerkleTree, HipMerkleTreeMmcs, fold_rows_at, fold_rows_device, lde_device,
-                  mle_eval)
+from .configs import (SEED_CHALLENGES, SEED_DATA, SEED_OOD, SEED_QUERIES, SEED_WEIGHTS, Workload,
+                      XorShift64, challenges, ef_pow2_chain, query_indices)
+from .pcs import (HipMerkleTree, HipMerkleTreeMmcs, eq_table, fold_rows_at, fold_rows_device, lde_device,
+                  mle_eval, sumcheck_prove)
 from ._native import DeviceBuffer
 
 
@@ -42,6 +46,8 @@ class RoundOutput:
     ood_answers: list = field(default_factory=list)  # table evaluations at z^(2^i)
     stir_indices: np.ndarray | None = None  # rows of the previous codeword opened this round
     stir_folds: np.ndarray | None = None    # their row folds with this round's challenges
+    weight_point: np.ndarray | None = None  # EF point of the sumcheck's evaluation constraint
+    sumcheck_polys: np.ndarray | None = None  # (k, 3, 2) round polynomials that folded the table
 
 
 @dataclass
@@ -91,17 +97,23 @@ def run_workload(wl: Workload, d_in: DeviceBuffer, with_openings: bool = True,
     if wl.rounds:
         ch = challenges(k * wl.rounds)
         g_ood, g_stir = XorShift64(SEED_OOD), XorShift64(SEED_QUERIES + 100)
+        g_w = XorShift64(SEED_WEIGHTS)
         table, t_rows, ext = d_in, wl.rows, False
         for r in range(wl.rounds):
             chr_ = ch[k * r:k * (r + 1)]
-            folded = DeviceBuffer(2 * t_rows)
-            fold_rows_device(table, t_rows, k, chr_, ext, folded, stream=stream)
+            # k sumcheck rounds fold the table (t_rows x 2^k entries) over its
+            # low k variables
+            t_vars = (t_rows.bit_length() - 1) + k
+            zw = np.array([g_w.field(), g_w.field()], np.uint64)
+            w_point = ef_pow2_chain(zw, t_vars)
+            polys, folded, _ = sumcheck_prove(table, ext, eq_table(w_point, stream), t_vars, chr_, stream)
             out.tables.append((folded, t_rows))
             prev = out.rounds[-1]
             table, ext = folded, True
             n_vars = (t_rows.bit_length() - 1)  # the folded table holds t_rows EF entries
             t_rows = t_rows >> k  # EF table of t_rows entries -> rows of 2^k EF
             rnd = commit_round(folded, t_rows, 2 << k, wl.log_blowup, mmcs, stream=stream)
+            rnd.weight_point, rnd.sumcheck_polys = w_point, polys
             for _ in range(2):
                 z = np.array([g_ood.field(), g_ood.field()], np.uint64)
                 rnd.ood_points.append(z)
