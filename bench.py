@@ -36,6 +36,10 @@ def parse():
     ap.add_argument("--prover-data", action="store_true",
                     help="after the timed steps, also time streaming the committed tree out of "
                          "HBM in the batch-cache prover-data format into a discarding host sink")
+    ap.add_argument("--sumcheck", action="store_true",
+                    help="after the timed steps, also time the WHIR round's sumcheck (k rounds over "
+                         "the 2^22-entry table of the opening-pipeline workload times an eq weight "
+                         "table) against the HBM roofline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the run, copy MIB MiB device to device three times (a plain "
                          "copy kernel of known size for scaling rocprofv3 FETCH/WRITE_SIZE)")
@@ -93,6 +97,45 @@ def prover_data_stream(N, d_cw, n: int, w: int, d_layers, stream, reps: int = 2)
     dt = (time.perf_counter() - t0) / reps
     return {"bytes": size, "ms": round(dt * 1e3, 3), "GB_per_s": round(size / dt / 1e9, 2),
             "sink": "discard", "path": "HBM -> pinned staging (2 x 16 MiB) -> host callback"}
+
+
+def sumcheck_rounds(N, stream, t: int = 22, k: int = 4, reps: int = 20):
+    """Time zkie_sumcheck_prove: k rounds over a base table of 2^t entries
+    times an EF weight table (the first round of the opening-pipeline
+    workload), per kernel with the library's HIP-event timers. Algorithmic
+    bytes per round on 2^m entries: the round kernel and the fold kernel each
+    read both tables (f: 8 B base in round 0, then 16 B EF; h: 16 B) and the
+    fold writes the two halved EF tables."""
+    import numpy as np
+
+    from zkie_amd import configs as C
+    from zkie_amd.pcs import eq_table, sumcheck_prove
+    from zkie_amd._native import DeviceBuffer
+
+    d_f = DeviceBuffer.from_array(N.gen_inputs(C.SEED_DATA, 1 << t, 0))  # uniform
+    d_h = eq_table(C.ef_pow2_chain(np.array([5, 6], np.uint64), t), stream.handle)
+    r = C.challenges(k)
+    sumcheck_prove(d_f, False, d_h, t, r, stream.handle)  # first use
+    N.check(N.load().zkie_device_synchronize(), "sync")
+    N.profile_enable(True)
+    N.profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        sumcheck_prove(d_f, False, d_h, t, r, stream.handle)
+    dt = (time.perf_counter() - t0) / reps
+    kern = {name: N.profile_query(name) for name in ("sumcheck_round", "sumcheck_fold")}
+    N.profile_enable(False)
+    alg = 0
+    for i in range(k):
+        m = t - i
+        fb = 8 if i == 0 else 16
+        alg += 2 * (1 << m) * (fb + 16) + (1 << (m - 1)) * 32
+    dev_ms = sum(ms for _, ms in kern.values()) / reps
+    return {"table": f"2^{t} base x EF weights", "rounds": k, "ms_per_call": round(dt * 1e3, 3),
+            "kernel_ms_per_call": round(dev_ms, 3), "alg_bytes": alg,
+            "GB_per_s_kernels": round(alg / (dev_ms * 1e-3) / 1e9, 1) if dev_ms else None,
+            "hbm_frac_kernels": round(alg / (dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if dev_ms else None,
+            "per_kernel_avg_ms": {n_: round(ms / max(c, 1), 4) for n_, (c, ms) in kern.items()}}
 
 
 def leaf_profile():
@@ -216,6 +259,8 @@ def main():
     }
     if args.prover_data:
         out["prover_data_stream"] = prover_data_stream(N, d_cw, n, w, d_layers, stream)
+    if args.sumcheck:
+        out["sumcheck"] = sumcheck_rounds(N, stream)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
         # single-threaded, on a sample 16x smaller (the reference quotes its GPU
