@@ -10,13 +10,17 @@
  *                               merkle_tree.rs:32-70), kept in device memory;
  *   zkie::fold_rows, zkie::mle_eval <- the WHIR row fold and out-of-domain
  *                               evaluation (p3-whir prover/mod.rs:226-290);
+ *   zkie::sumcheck_prove     <- sumcheck::prove (crates/zkie-core/src/common/
+ *                               sumcheck.rs:33-79) over a device table and
+ *                               weight table, EF rounds;
  *   zkie::serialize_batch_prover_data_into, zkie::restore_batch_prover_data_from
  *                            <- the prover-data part of the batch cache
  *                               (crates/zkie-core/src/pcs/whir.rs:542-602).
  * Matrices are p3's RowMajorMatrix<F> (values row-major, canonical u64).
  * Errors: every non-zero status of the C ABI throws zkie::Error carrying it;
  * there is no CPU fallback here (the reference's Rust caller keeps its own,
- * dft_cuda.rs:174-177). Calls on one device are serialised by the caller. */
+ * dft_cuda.rs:174-177). Calls may come from several host threads: the
+ * library orders its own scratch buffers between them. */
 #pragma once
 
 #include <array>
@@ -289,6 +293,39 @@ inline Ef mle_eval(const DeviceBuffer& d_vals, uint32_t num_vars, bool is_ext, c
     Ef out{};
     check(zkie_mle_eval(d_vals.data(), num_vars, is_ext ? 1 : 0, ef_ptr(r), out.data(), nullptr), "zkie_mle_eval");
     return out;
+}
+
+/* sumcheck::prove's result (sumcheck.rs:10-30) with EF values: one round
+ * polynomial c0 + c1 X + c2 X^2 per round and the two tables' final values. */
+struct RoundPoly {
+    Ef c0, c1, c2;
+};
+struct SumcheckProof {
+    std::vector<RoundPoly> rounds;
+    Ef f_eval, h_eval;
+};
+
+/* sumcheck::prove (sumcheck.rs:33-79) of sum_x f(x) h(x) over device tables of
+ * 2^num_vars entries (f base or EF, h EF) with the challenges given up front,
+ * one per variable. */
+inline SumcheckProof sumcheck_prove(const DeviceBuffer& d_f, bool f_is_ext, const DeviceBuffer& d_h,
+                                    uint32_t num_vars, const std::vector<Ef>& challenges)
+{
+    if (challenges.size() != num_vars) throw Error(ZKIE_ERR_INVALID, "sumcheck challenges");
+    std::vector<F> polys(6 * (num_vars ? num_vars : 1));
+    DeviceBuffer f_out(2), h_out(2);
+    check(zkie_sumcheck_prove(d_f.data(), f_is_ext ? 1 : 0, d_h.data(), num_vars, num_vars,
+                              num_vars ? ef_ptr(challenges) : polys.data(), polys.data(), f_out.data(),
+                              h_out.data(), nullptr),
+          "zkie_sumcheck_prove");
+    SumcheckProof p;
+    for (uint32_t i = 0; i < num_vars; i++)
+        p.rounds.push_back({Ef{polys[6 * i], polys[6 * i + 1]}, Ef{polys[6 * i + 2], polys[6 * i + 3]},
+                            Ef{polys[6 * i + 4], polys[6 * i + 5]}});
+    const std::vector<F> fe = f_out.download(), he = h_out.download();
+    p.f_eval = {fe[0], fe[1]};
+    p.h_eval = {he[0], he[1]};
+    return p;
 }
 
 }  // namespace zkie

@@ -109,6 +109,26 @@ int main()
     same = true;
     for (size_t i = 0; i < h; i++) same = same && f[i][0] == fref[2 * i] && f[i][1] == fref[2 * i + 1];
     EXPECT(same, "fold_rows equals the oracle");
+
+    // sumcheck::prove over the committed codeword's first 2^12 entries and an EF weight table
+    {
+        const uint32_t t = 12;
+        std::vector<F> fv(cw.values.begin(), cw.values.begin() + (size_t(1) << t));
+        std::vector<F> hv(size_t(2) << t);
+        or_gen_uniform(77, hv.size(), hv.data());
+        std::vector<zkie::Ef> ch(t);
+        for (uint32_t b = 0; b < t; b++) ch[b] = {F(31 * b + 5), F(b + 2)};
+        const zkie::DeviceBuffer d_f = zkie::DeviceBuffer::upload(fv), d_h = zkie::DeviceBuffer::upload(hv);
+        const zkie::SumcheckProof pr = zkie::sumcheck_prove(d_f, false, d_h, t, ch);
+        std::vector<F> polys(6 * t), fo(2), ho(2);
+        or_sumcheck_prove(fv.data(), 0, hv.data(), t, t, &ch[0][0], polys.data(), fo.data(), ho.data());
+        same = pr.rounds.size() == t && pr.f_eval == zkie::Ef{fo[0], fo[1]} && pr.h_eval == zkie::Ef{ho[0], ho[1]};
+        for (uint32_t i = 0; same && i < t; i++)
+            same = pr.rounds[i].c0 == zkie::Ef{polys[6 * i], polys[6 * i + 1]} &&
+                   pr.rounds[i].c1 == zkie::Ef{polys[6 * i + 2], polys[6 * i + 3]} &&
+                   pr.rounds[i].c2 == zkie::Ef{polys[6 * i + 4], polys[6 * i + 5]};
+        EXPECT(same, "sumcheck_prove equals the oracle");
+    }
     bool threw = false;
 
     // prover-data cache stream (whir.rs:542-602): framing, payload, round trip
