@@ -103,9 +103,10 @@ def sumcheck_rounds(N, stream, t: int = 22, k: int = 4, reps: int = 20):
     """Time zkie_sumcheck_prove: k rounds over a base table of 2^t entries
     times an EF weight table (the first round of the opening-pipeline
     workload), per kernel with the library's HIP-event timers. Algorithmic
-    bytes per round on 2^m entries: the round kernel and the fold kernel each
-    read both tables (f: 8 B base in round 0, then 16 B EF; h: 16 B) and the
-    fold writes the two halved EF tables."""
+    bytes: round 0's sums read both tables (f: 8 B per base entry, h: 16 B),
+    then every round's fold reads both tables (f: 8 B in round 0, then 16 B
+    EF) and writes the two halved EF tables, the folds before the last one
+    forming the next round's sums in the same pass."""
     import numpy as np
 
     from zkie_amd import configs as C
@@ -123,13 +124,14 @@ def sumcheck_rounds(N, stream, t: int = 22, k: int = 4, reps: int = 20):
     for _ in range(reps):
         sumcheck_prove(d_f, False, d_h, t, r, stream.handle)
     dt = (time.perf_counter() - t0) / reps
-    kern = {name: N.profile_query(name) for name in ("sumcheck_round", "sumcheck_fold")}
+    kern = {name: N.profile_query(name) for name in ("sumcheck_round", "sumcheck_fold_round", "sumcheck_fold",
+                                                  "sumcheck_finish")}
     N.profile_enable(False)
-    alg = 0
+    alg = (1 << t) * (8 + 16)
     for i in range(k):
         m = t - i
         fb = 8 if i == 0 else 16
-        alg += 2 * (1 << m) * (fb + 16) + (1 << (m - 1)) * 32
+        alg += (1 << m) * (fb + 16) + (1 << (m - 1)) * 32
     dev_ms = sum(ms for _, ms in kern.values()) / reps
     return {"table": f"2^{t} base x EF weights", "rounds": k, "ms_per_call": round(dt * 1e3, 3),
             "kernel_ms_per_call": round(dev_ms, 3), "alg_bytes": alg,

@@ -188,9 +188,13 @@ int zkie_sumcheck_round(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, 
                         uint64_t *poly, void *stream);
 /* zkie_sumcheck_fold: both tables bound at variable 0 to r (host, one EF);
  * d_f_out and d_h_out receive 2^(num_vars-1) EF entries each and must not
- * overlap the inputs or each other. Does not synchronise. */
+ * overlap the inputs or each other. With next_poly (host, 6 u64) non-NULL
+ * (num_vars >= 2) the same pass also forms the next round's polynomial, as
+ * zkie_sumcheck_round on the outputs would, and the call synchronises;
+ * with next_poly NULL it does not. */
 int zkie_sumcheck_fold(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, uint32_t num_vars,
-                       const uint64_t *r, uint64_t *d_f_out, uint64_t *d_h_out, void *stream);
+                       const uint64_t *r, uint64_t *d_f_out, uint64_t *d_h_out, uint64_t *next_poly,
+                       void *stream);
 /* zkie_eq_table: the weight table of one evaluation constraint,
  * d_out[x] = eq(point, x) = prod_b (x_b ? p_b : 1 - p_b) for x < 2^num_vars
  * (EF, bit 0 of x first, mle.rs:44-56), so that sum_x eq(p, x) f(x) = f(p)

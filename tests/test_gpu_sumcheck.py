@@ -52,6 +52,15 @@ def test_round_entries_compose(native, oracle, f_ext):
         d_f, d_h = pcs.sumcheck_fold(d_f, ext, d_h, t - i, r[i])
         ext = True
     assert (d_f.download().reshape(-1, 2) == wf).all() and (d_h.download().reshape(-1, 2) == wh).all()
+    # the fold that also forms the next round's polynomial in the same pass
+    d_f, d_h, ext = DeviceBuffer.from_array(f), DeviceBuffer.from_array(h), f_ext
+    assert (pcs.sumcheck_round(d_f, ext, d_h, t) == wp[0]).all()
+    for i in range(t - 1):
+        d_f, d_h, poly = pcs.sumcheck_fold(d_f, ext, d_h, t - i, r[i], next_poly=True)
+        assert (poly == wp[i + 1]).all(), i
+        ext = True
+    d_f, d_h = pcs.sumcheck_fold(d_f, ext, d_h, 1, r[t - 1])
+    assert (d_f.download().reshape(-1, 2) == wf).all() and (d_h.download().reshape(-1, 2) == wh).all()
 
 
 @pytest.mark.parametrize("f_ext", [False, True])
@@ -81,8 +90,10 @@ def test_rejects_overlap_and_bad_sizes(native, oracle):
     rr = np.ascontiguousarray(r[0])
     polys = np.zeros(6 * t, np.uint64)
     p = native.p
-    assert L.zkie_sumcheck_fold(d_f.addr, 1, d_h.addr, t, p(rr), d_f.addr, out.addr, None) == -1
-    assert L.zkie_sumcheck_fold(d_f.addr, 1, d_h.addr, t, p(rr), out.addr, out.addr + 8, None) == -1
+    assert L.zkie_sumcheck_fold(d_f.addr, 1, d_h.addr, t, p(rr), d_f.addr, out.addr, None, None) == -1
+    assert L.zkie_sumcheck_fold(d_f.addr, 1, d_h.addr, t, p(rr), out.addr, out.addr + 8, None, None) == -1
+    assert L.zkie_sumcheck_fold(d_f.addr, 1, d_h.addr, 1, p(rr), out.addr, out.addr + 64, p(polys),
+                                None) == -1
     assert L.zkie_sumcheck_round(d_f.addr, 1, d_h.addr, 0, p(polys), None) == -1
     rs = np.ascontiguousarray(r.reshape(-1))
     assert L.zkie_sumcheck_prove(d_f.addr, 1, d_h.addr, t, t + 1, p(rs), p(polys), out.addr,

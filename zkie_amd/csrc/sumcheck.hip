@@ -86,21 +86,44 @@ __global__ __launch_bounds__(kScThreads) void sc_round_kernel(const uint64_t* __
     }
 }
 
-// One workgroup: the sum of `nblocks` partial records into out[0..6).
-__global__ __launch_bounds__(kScThreads) void sc_finish_kernel(const uint64_t* __restrict__ partial,
-                                                               uint32_t nblocks, uint64_t* __restrict__ out)
+// One workgroup of kFinThreads: the sum of `nblocks` partial records into
+// out[0..6). Thread t adds component t % 6 of the records t / 6,
+// t / 6 + kFinThreads / 6, ... (consecutive threads read consecutive words),
+// then the kFinThreads / 6 threads of each component reduce in LDS.
+// Workgroup g handles the records of round g: counts.n[g] records from
+// partial + g * 6 * kScMaxBlocks, sums to out + 6 g.
+constexpr int kFinThreads = 768;
+constexpr int kFinPer = kFinThreads / 6;
+constexpr uint32_t kScMaxRounds = 34;
+
+struct FinCounts {
+    uint32_t n[kScMaxRounds];
+};
+
+__global__ __launch_bounds__(kFinThreads) void sc_finish_kernel(const uint64_t* __restrict__ partial,
+                                                                const FinCounts counts, uint64_t* __restrict__ out)
 {
-    __shared__ uint64_t red[6][kScThreads];
-    uint64_t v[6] = {0, 0, 0, 0, 0, 0};
-    for (uint32_t b = threadIdx.x; b < nblocks; b += kScThreads) {
-#pragma unroll
-        for (int e = 0; e < 6; e++) v[e] = gl_add(v[e], partial[6 * (uint64_t)b + e]);
+    __shared__ uint64_t red[kFinThreads];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nblocks = counts.n[blockIdx.x];
+    partial += 6ull * kScMaxBlocks * blockIdx.x;
+    out += 6 * blockIdx.x;
+    uint64_t v = 0;
+    for (uint64_t i = tid; i < 6ull * nblocks; i += kFinThreads) v = gl_add(v, partial[i]);
+    red[tid] = v;
+    __syncthreads();
+    // component e = tid % 6 of lane j = tid / 6 lives at red[6 j + e]
+    const uint32_t e = tid % 6, j = tid / 6;
+#pragma unroll 1
+    for (uint32_t w = kFinPer / 2; w > 0; w >>= 1) {
+        uint64_t x = 0;
+        const bool act = j < w;
+        if (act) x = gl_add(red[6 * j + e], red[6 * (j + w) + e]);
+        __syncthreads();
+        if (act) red[6 * j + e] = x;
+        __syncthreads();
     }
-    sc_block_reduce(v, red);
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int e = 0; e < 6; e++) out[e] = gl_canon(v[e]);
-    }
+    if (tid < 6) out[tid] = gl_canon(red[tid]);
 }
 
 // Both tables bound at variable 0: out[s] = a[2s] + r (a[2s + 1] - a[2s]),
@@ -125,21 +148,104 @@ __global__ __launch_bounds__(kScThreads) void sc_fold_kernel(const uint64_t* __r
     h_out[2 * s + 1] = gl_canon(ho.c1);
 }
 
-// Round sums of tables of 2^m entries (m >= 1) into d_sums (6 u64), using
-// `partial` (kScMaxBlocks records of 6 u64).
+// Bind variable 0 of both tables (2^m entries, m >= 2) to r and, in the
+// same pass, the next round's partial sums over the folded tables: lane s
+// reads entries 4s .. 4s + 3, writes folded entries 2s and 2s + 1 (one pair
+// of the next round) and adds that pair's y0, y1, y2.
+template <bool FEXT>
+__global__ __launch_bounds__(kScThreads) void sc_fold_round_kernel(const uint64_t* __restrict__ f,
+                                                                   const uint64_t* __restrict__ h,
+                                                                   uint64_t quarter, uint64_t r0, uint64_t r1,
+                                                                   uint64_t* __restrict__ f_out,
+                                                                   uint64_t* __restrict__ h_out,
+                                                                   uint64_t* __restrict__ partial)
+{
+    __shared__ uint64_t red[6][kScThreads];
+    const Ef r{r0, r1};
+    Ef y0{0, 0}, y1{0, 0}, y2{0, 0};
+    const uint64_t stride = (uint64_t)gridDim.x * kScThreads;
+    for (uint64_t s = (uint64_t)blockIdx.x * kScThreads + threadIdx.x; s < quarter; s += stride) {
+        Ef fa[4], ha[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            fa[q] = sc_load_f<FEXT>(f, 4 * s + q);
+            ha[q] = Ef{h[8 * s + 2 * q], h[8 * s + 2 * q + 1]};
+        }
+        const Ef f0 = ef_add(fa[0], ef_mul(r, ef_sub(fa[1], fa[0])));
+        const Ef f1 = ef_add(fa[2], ef_mul(r, ef_sub(fa[3], fa[2])));
+        const Ef h0 = ef_add(ha[0], ef_mul(r, ef_sub(ha[1], ha[0])));
+        const Ef h1 = ef_add(ha[2], ef_mul(r, ef_sub(ha[3], ha[2])));
+        f_out[4 * s] = gl_canon(f0.c0);
+        f_out[4 * s + 1] = gl_canon(f0.c1);
+        f_out[4 * s + 2] = gl_canon(f1.c0);
+        f_out[4 * s + 3] = gl_canon(f1.c1);
+        h_out[4 * s] = gl_canon(h0.c0);
+        h_out[4 * s + 1] = gl_canon(h0.c1);
+        h_out[4 * s + 2] = gl_canon(h1.c0);
+        h_out[4 * s + 3] = gl_canon(h1.c1);
+        const Ef f2 = ef_sub(ef_add(f1, f1), f0), h2 = ef_sub(ef_add(h1, h1), h0);
+        y0 = ef_add(y0, ef_mul(f0, h0));
+        y1 = ef_add(y1, ef_mul(f1, h1));
+        y2 = ef_add(y2, ef_mul(f2, h2));
+    }
+    uint64_t v[6] = {y0.c0, y0.c1, y1.c0, y1.c1, y2.c0, y2.c1};
+    sc_block_reduce(v, red);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int e = 0; e < 6; e++) partial[6 * (uint64_t)blockIdx.x + e] = gl_canon(v[e]);
+    }
+}
+
+uint32_t sc_blocks(uint64_t items)
+{
+    const uint64_t want = (items + kScThreads - 1) / kScThreads;
+    return (uint32_t)(want < kScMaxBlocks ? want : kScMaxBlocks);
+}
+
+// Adds the `blocks` partial records at `partial` into d_sums (6 u64).
+int sc_finish(const uint64_t* partial, uint32_t blocks, uint64_t* d_sums, hipStream_t s)
+{
+    FinCounts c{};
+    c.n[0] = blocks;
+    ProfMark pm = prof_begin("sumcheck_finish", s);
+    sc_finish_kernel<<<1, kFinThreads, 0, s>>>(partial, c, d_sums);
+    prof_end(pm, s);
+    ZK_LAUNCHED();
+    return ZKIE_OK;
+}
+
+// Partial round sums of tables of 2^m entries (m >= 1) into `partial`
+// (kScMaxBlocks records of 6 u64); *blocks receives the record count.
 int sc_sums(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, uint64_t* partial,
-            uint64_t* d_sums, hipStream_t s)
+            uint32_t* blocks, hipStream_t s)
 {
     const uint64_t half = 1ull << (m - 1);
-    const uint64_t want = (half + kScThreads - 1) / kScThreads;
-    const uint32_t blocks = (uint32_t)(want < kScMaxBlocks ? want : kScMaxBlocks);
+    *blocks = sc_blocks(half);
     ProfMark pm = prof_begin("sumcheck_round", s);
     if (f_ext)
-        sc_round_kernel<true><<<blocks, kScThreads, 0, s>>>(d_f, d_h, half, partial);
+        sc_round_kernel<true><<<*blocks, kScThreads, 0, s>>>(d_f, d_h, half, partial);
     else
-        sc_round_kernel<false><<<blocks, kScThreads, 0, s>>>(d_f, d_h, half, partial);
+        sc_round_kernel<false><<<*blocks, kScThreads, 0, s>>>(d_f, d_h, half, partial);
+    prof_end(pm, s);
     ZK_LAUNCHED();
-    sc_finish_kernel<<<1, kScThreads, 0, s>>>(partial, blocks, d_sums);
+    return ZKIE_OK;
+}
+
+// Fold of tables of 2^m entries (m >= 2) by r with the next round's partial
+// sums into `partial`; *blocks receives the record count.
+int sc_fold_sums(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, const uint64_t* r,
+                 uint64_t* d_f_out, uint64_t* d_h_out, uint64_t* partial, uint32_t* blocks, hipStream_t s)
+{
+    const uint64_t quarter = 1ull << (m - 2);
+    *blocks = sc_blocks(quarter);
+    const uint64_t r0 = gl_canon(r[0]), r1 = gl_canon(r[1]);
+    ProfMark pm = prof_begin("sumcheck_fold_round", s);
+    if (f_ext)
+        sc_fold_round_kernel<true><<<*blocks, kScThreads, 0, s>>>(d_f, d_h, quarter, r0, r1, d_f_out, d_h_out,
+                                                                  partial);
+    else
+        sc_fold_round_kernel<false><<<*blocks, kScThreads, 0, s>>>(d_f, d_h, quarter, r0, r1, d_f_out, d_h_out,
+                                                                   partial);
     prof_end(pm, s);
     ZK_LAUNCHED();
     return ZKIE_OK;
@@ -227,7 +333,9 @@ int zkie_sumcheck_round(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, 
     if (ws.status()) return ws.status();
     uint64_t* partial = (uint64_t*)ws.get();
     uint64_t* d_sums = partial + 6 * kScMaxBlocks;
-    int rc = sc_sums(d_f, f_is_ext != 0, d_h, num_vars, partial, d_sums, s);
+    uint32_t blocks = 0;
+    int rc = sc_sums(d_f, f_is_ext != 0, d_h, num_vars, partial, &blocks, s);
+    if (!rc) rc = sc_finish(partial, blocks, d_sums, s);
     if (rc) return rc;
     uint64_t y[6];
     ZK_TRY(hipMemcpyAsync(y, d_sums, sizeof(y), hipMemcpyDeviceToHost, s));
@@ -237,16 +345,32 @@ int zkie_sumcheck_round(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, 
 }
 
 int zkie_sumcheck_fold(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, uint32_t num_vars,
-                       const uint64_t* r, uint64_t* d_f_out, uint64_t* d_h_out, void* stream)
+                       const uint64_t* r, uint64_t* d_f_out, uint64_t* d_h_out, uint64_t* next_poly,
+                       void* stream)
 {
     if (num_vars < 1 || num_vars > 34 || !d_f || !d_h || !r || !d_f_out || !d_h_out) return ZKIE_ERR_INVALID;
+    if (next_poly && num_vars < 2) return ZKIE_ERR_INVALID;
     const uint64_t n = 1ull << num_vars, half = n >> 1;
     const uint64_t nf = f_is_ext ? 2 * n : n;
     if (overlaps(d_f_out, 2 * half, d_f, nf) || overlaps(d_f_out, 2 * half, d_h, 2 * n) ||
         overlaps(d_h_out, 2 * half, d_f, nf) || overlaps(d_h_out, 2 * half, d_h, 2 * n) ||
         overlaps(d_f_out, 2 * half, d_h_out, 2 * half))
         return ZKIE_ERR_INVALID;
-    return sc_fold(d_f, f_is_ext != 0, d_h, num_vars, r, d_f_out, d_h_out, as_stream(stream));
+    hipStream_t s = as_stream(stream);
+    if (!next_poly) return sc_fold(d_f, f_is_ext != 0, d_h, num_vars, r, d_f_out, d_h_out, s);
+    Scratch ws(WS_MISC, (kScMaxBlocks + 1) * 6 * 8, s);
+    if (ws.status()) return ws.status();
+    uint64_t* partial = (uint64_t*)ws.get();
+    uint64_t* d_sums = partial + 6 * kScMaxBlocks;
+    uint32_t blocks = 0;
+    int rc = sc_fold_sums(d_f, f_is_ext != 0, d_h, num_vars, r, d_f_out, d_h_out, partial, &blocks, s);
+    if (!rc) rc = sc_finish(partial, blocks, d_sums, s);
+    if (rc) return rc;
+    uint64_t y[6];
+    ZK_TRY(hipMemcpyAsync(y, d_sums, sizeof(y), hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    sc_coefficients(y, next_poly);
+    return ZKIE_OK;
 }
 
 int zkie_eq_table(const uint64_t* point, uint32_t num_vars, uint64_t* d_out, void* stream)
@@ -300,18 +424,22 @@ int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, 
     // B after it (at most half / 2 entries each: 2 half u64).
     const uint64_t half = n >> 1;
     const uint64_t pool_u64 = rounds > 1 ? 6 * half : 0;
-    Scratch ws(WS_FOLD, (6 * (kScMaxBlocks + rounds) + pool_u64) * 8, s);
+    // Every round keeps its own partial records, added by one launch at the end.
+    Scratch ws(WS_FOLD, (6 * (kScMaxBlocks + 1) * rounds + pool_u64) * 8, s);
     if (ws.status()) return ws.status();
     uint64_t* partial = (uint64_t*)ws.get();
-    uint64_t* d_y = partial + 6 * kScMaxBlocks;
+    uint64_t* d_y = partial + 6 * kScMaxBlocks * rounds;
     uint64_t* pool = d_y + 6 * rounds;
+    FinCounts counts{};
     const uint64_t* cf = d_f;
     const uint64_t* ch = d_h;
     bool ext = f_is_ext != 0;
+    // round 0's sums, then each fold computes the next round's sums in the
+    // same pass; the last fold is a plain one
+    int rc = sc_sums(cf, ext, ch, num_vars, partial, &counts.n[0], s);
+    if (rc) return rc;
     for (uint32_t i = 0; i < rounds; i++) {
         const uint32_t m = num_vars - i;
-        int rc = sc_sums(cf, ext, ch, m, partial, d_y + 6 * i, s);
-        if (rc) return rc;
         uint64_t *nf_, *nh_;
         if (i + 1 == rounds) {
             nf_ = d_f_out;
@@ -322,12 +450,20 @@ int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, 
             nf_ = base;
             nh_ = base + (i % 2 == 0 ? 2 * half : half);
         }
-        rc = sc_fold(cf, ext, ch, m, r + 2 * i, nf_, nh_, s);
+        if (i + 1 < rounds)  // m >= 2 here, since rounds <= num_vars
+            rc = sc_fold_sums(cf, ext, ch, m, r + 2 * i, nf_, nh_, partial + 6ull * kScMaxBlocks * (i + 1),
+                              &counts.n[i + 1], s);
+        else
+            rc = sc_fold(cf, ext, ch, m, r + 2 * i, nf_, nh_, s);
         if (rc) return rc;
         cf = nf_;
         ch = nh_;
         ext = true;
     }
+    ProfMark pm = prof_begin("sumcheck_finish", s);
+    sc_finish_kernel<<<rounds, kFinThreads, 0, s>>>(partial, counts, d_y);
+    prof_end(pm, s);
+    ZK_LAUNCHED();
     std::vector<uint64_t> y(6 * rounds);
     ZK_TRY(hipMemcpyAsync(y.data(), d_y, y.size() * 8, hipMemcpyDeviceToHost, s));
     ZK_TRY(hipStreamSynchronize(s));

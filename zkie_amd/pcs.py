@@ -234,16 +234,20 @@ def eq_table(point, stream=None) -> DeviceBuffer:
 
 
 def sumcheck_fold(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int, r,
-                  stream=None) -> tuple[DeviceBuffer, DeviceBuffer]:
+                  stream=None, next_poly: bool = False):
     """Both tables bound at variable 0 to the EF challenge r
-    (common/sumcheck.rs:81-89); returns the two folded EF tables."""
+    (common/sumcheck.rs:81-89); returns the two folded EF tables, and with
+    next_poly also the next round's polynomial formed in the same pass."""
     rr = np.ascontiguousarray(np.asarray(r, np.uint64).reshape(-1))
     assert rr.size == 2
     half = 1 << (num_vars - 1)
     f_out, h_out = DeviceBuffer(2 * half), DeviceBuffer(2 * half)
+    poly = np.zeros((3, 2), np.uint64)
     check(N.load().zkie_sumcheck_fold(d_f.addr, 1 if f_is_ext else 0, d_h.addr, num_vars, N.p(rr),
-                                      f_out.addr, h_out.addr, stream), "zkie_sumcheck_fold")
-    return f_out, h_out
+                                      f_out.addr, h_out.addr,
+                                      N.p(poly) if next_poly else ctypes.cast(0, N._u64p), stream),
+          "zkie_sumcheck_fold")
+    return (f_out, h_out, poly) if next_poly else (f_out, h_out)
 
 
 def sumcheck_prove(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int, r,
