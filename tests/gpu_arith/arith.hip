@@ -13,7 +13,7 @@ using namespace zk;
 
 namespace {
 
-constexpr int kOps = 10;
+constexpr int kOps = 11;
 
 __global__ void binary_kernel(const uint64_t* a, const uint64_t* b, uint64_t* out, uint64_t n)
 {
@@ -34,8 +34,9 @@ __global__ void binary_kernel(const uint64_t* a, const uint64_t* b, uint64_t* ou
     gl_fold_eps(r, w);
     o[8] = gl_canon(r);
     uint64_t p, q;
-    gl_mul2(x, y, y, x, p, q);
-    o[9] = gl_canon(gl_sub2(p, q));  // 0
+    gl_mul2(x, y, x, x, p, q);  // two different products through the interleaved form
+    o[9] = gl_canon(p);
+    o[10] = gl_canon(q);
 }
 
 // st: n states of 16 words; mode 0 mds_light16, 1 internal round (rc, diag15

@@ -35,6 +35,15 @@ def _edge_values():
     return sorted(v)
 
 
+def _mid_carry(a, b):
+    """1 when X.hi + k = 2^32 for X = a1 b0 + a0 b1 mod 2^64 and k the carry
+    of P.hi + X.lo, P = a0 b0 (32-bit halves a = a0 + a1 2^32)."""
+    a0, a1, b0, b1 = a & 0xFFFFFFFF, a >> 32, b & 0xFFFFFFFF, b >> 32
+    x = (a1 * b0 + a0 * b1) & M
+    k = (((a0 * b0) >> 32) + (x & 0xFFFFFFFF)) >> 32
+    return ((x >> 32) + k) >> 32
+
+
 def test_binary_ops_on_edges_and_random(native):
     print("CASE gpu arith binary", flush=True)
     L = _lib()
@@ -46,6 +55,15 @@ def test_binary_ops_on_edges_and_random(native):
     # products that are a multiple of 2^96 plus a little (the reduction's borrow)
     pairs += [(1 << a, 1 << (96 - a)) for a in range(33, 64)]
     pairs += [((1 << a) + 1, 1 << (96 - a)) for a in range(33, 64)]
+    # products and squares whose middle partial products sum to just below
+    # 2^64 (X = a1 b0 + a0 b1 with X.hi = 2^32 - 1) and take a carry from
+    # P.hi + X.lo (P = a0 b0): the product's 2^96 term is formed from carries
+    mid = [((a1 << 32) | 0xFFFFFFFF, ((2**32 + 1 - a1) << 32) | 0xFFFFFFFF) for a1 in range(2, 2**32, 2**32 // 64)]
+    sq = sorted({(((((2**64 - 2**32 + j) // (2 * a0)) & 0xFFFFFFFF) + 1) << 32) | a0
+                 for a0 in range(2**32 - 256, 2**32) for j in range(0, 2**32, 2**28)})
+    sq = [s for s in sq if _mid_carry(s, s)]
+    assert sum(_mid_carry(x, y) for x, y in mid) == len(mid) and len(sq) >= 64
+    pairs += mid + [(s, s) for s in sq[:256]]
     a = np.array([x for x, _ in pairs], np.uint64)
     b = np.array([y for _, y in pairs], np.uint64)
     out = np.zeros(len(pairs) * k, np.uint64)
@@ -54,7 +72,7 @@ def test_binary_ops_on_edges_and_random(native):
     i24 = pow(1 << 24, P - 2, P)
     for n, (x, y) in enumerate(pairs):
         want = [(x + y) % P, (x - y) % P, x * y % P, x * x % P, (x << 24) % P, (x << 48) % P, x * i24 % P,
-                ((x >> 29) + ((y >> 29) << 32)) % P, ((x >> 29) + ((y >> 29) << 32)) % P, 0]
+                ((x >> 29) + ((y >> 29) << 32)) % P, ((x >> 29) + ((y >> 29) << 32)) % P, x * y % P, x * x % P]
         got = [int(v) for v in out[n]]
         assert got == want, (hex(x), hex(y), got, want)
 
