@@ -140,6 +140,18 @@ def sumcheck_rounds(N, stream, t: int = 22, k: int = 4, reps: int = 20):
             "per_kernel_avg_ms": {n_: round(ms / max(c, 1), 4) for n_, (c, ms) in kern.items()}}
 
 
+def h2d_seconds(N, d_in, data, reps: int = 2) -> float:
+    """Mean time of a synchronous upload of the step's input (8 B per
+    element) from pageable host memory into its device buffer."""
+    d_in.upload(data)  # first use of these host pages
+    N.check(N.load().zkie_device_synchronize(), "sync")
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        d_in.upload(data)
+    N.check(N.load().zkie_device_synchronize(), "sync")
+    return (time.perf_counter() - t0) / reps
+
+
 def leaf_profile():
     """Per-launch figures of the leaf kernel measured with rocprofv3 at this
     workload: HBM bytes (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) and VALU
@@ -167,7 +179,6 @@ def main():
     assert N.device_count() >= 1, "no HIP device"
     data = N.gen_inputs(C.SEED_DATA, wl.elems, wl.kind)
     d_in = DeviceBuffer.from_array(data)
-    del data
     n, w = wl.codeword_rows, wl.cols
     d_cw = DeviceBuffer(n * w)
     lens = N.merkle_layout(n)
@@ -198,6 +209,8 @@ def main():
     t = (time.perf_counter() - t0) / args.steps
     per_kernel = {k: N.profile_query(k) for k in N.profile_names()}
     N.profile_enable(False)
+    h2d_s = h2d_seconds(N, d_in, data)
+    del data
 
     value = wl.elems / t
     # Dominant kernel: the Merkle leaf hash (2 of the 3 permutations per row).
@@ -258,6 +271,13 @@ def main():
                           if prof.get("valu_per_launch") and leaf_avg_ms else None),
         "stage_ms_per_step": stage_ms,
         "stages": stages,
+        # A caller that hands over the input in host memory (the reference's
+        # dft_batch takes a host RowMajorMatrix) also pays its upload; the
+        # tree stays in HBM and only the root comes back (inside the step).
+        "pcie_inclusive": {"value": wl.elems / (t + h2d_s), "unit": "elem/s",
+                           "h2d_ms": round(h2d_s * 1e3, 3),
+                           "h2d_GB_per_s": round(wl.elems * 8 / h2d_s / 1e9, 2),
+                           "source": "pageable host memory (numpy), synchronous copy"},
     }
     if args.prover_data:
         out["prover_data_stream"] = prover_data_stream(N, d_cw, n, w, d_layers, stream)
