@@ -103,7 +103,14 @@ def ef_pow2_chain(z, n: int) -> np.ndarray:
 
 
 def query_indices(count: int, height: int, g: XorShift64) -> np.ndarray:
-    """`count` draws of next_u64() mod height, sorted and deduplicated
-    (get_challenge_stir_queries returns sorted distinct indices,
-    p3-whir src/pcs/utils.rs:70-119)."""
-    return np.array(sorted({g.next_u64() % height for _ in range(count)}), np.uint64)
+    """min(count, height) distinct indices in [0, height), sorted ascending,
+    following get_challenge_stir_queries (p3-whir src/pcs/utils.rs:70-119):
+    draw uniform indices (next_u64() mod height: the low log2(height) bits,
+    height being a power of two), keep a draw only if it is new, until the
+    target count is reached (count >= height opens every row), then sort."""
+    assert height > 0 and height & (height - 1) == 0, "the folded domain size is a power of two"
+    target = min(count, height)
+    seen: set[int] = set()
+    while len(seen) < target:
+        seen.add(g.next_u64() % height)
+    return np.array(sorted(seen), np.uint64)
