@@ -86,3 +86,27 @@ def test_host_threads_share_the_library(native, oracle):
         th.join(timeout=120)
     assert not any(th.is_alive() for th in threads), "a worker thread did not finish"
     assert not errors, errors
+
+
+def test_coset_ldes_on_unordered_streams(native, oracle):
+    """Coset LDEs (shift != 1) queued on two streams with no waits between
+    them and no host synchronisation inside the calls: the coset powers are
+    formed on the device in the leased table of each call's stream."""
+    from zkie_amd import pcs
+    from zkie_amd._native import DeviceBuffer, Stream
+
+    print("CASE coset ldes on unordered streams", flush=True)
+    cases = [(1 << 12, 16, 2, 7), (1 << 13, 8, 1, 0x1234567890ABCDEF), (1 << 16, 1, 2, 11)]
+    streams = [Stream(), Stream()]
+    inputs, outs = [], []
+    for i, (h, w, lb, shift) in enumerate(cases):
+        x = oracle.gen_uniform(800 + i, h * w).reshape(h, w)
+        d_in, d_out = DeviceBuffer.from_array(x), DeviceBuffer((h << lb) * w)
+        pcs.lde_device(d_in, h, w, lb, d_out, shift=shift, stream=streams[i % 2].handle)
+        inputs.append((x, d_in))
+        outs.append(d_out)
+    for s in streams:
+        s.synchronize()
+    for (h, w, lb, shift), (x, _), d_out in zip(cases, inputs, outs):
+        got = d_out.download().reshape(h << lb, w)
+        assert (got == oracle.lde_batch(x, lb, shift % P)).all(), (h, w, lb, shift)

@@ -33,8 +33,13 @@ COMMON = [
 ]
 
 
-def _compile(src: str) -> str:
+def _compile(src: str, force: bool = True) -> str:
     obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
+    if not force and os.path.exists(obj):
+        deps = [os.path.join(CSRC, f) for f in os.listdir(CSRC)] + [os.path.join(ROOT, "include", "zkie_hip.h")]
+        if all(os.path.getmtime(obj) >= os.path.getmtime(d) for d in deps if d.endswith((".hpp", ".h"))) \
+                and os.path.getmtime(obj) >= os.path.getmtime(os.path.join(CSRC, src)):
+            return obj
     cmd = [HIPCC, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -42,10 +47,12 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, force: bool = True) -> str:
+    """Compile every source (force) or only those older than their sources
+    and the shared headers (force=False), then link."""
     os.makedirs(OUT_DIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, force), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -58,5 +65,5 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, force="--incremental" not in sys.argv)
     sys.exit(0)

@@ -122,6 +122,8 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
                 uint64_t* d_out, hipStream_t s)
 {
     if (k > 8 || !r || (h && (!d_mat || !d_out))) return ZKIE_ERR_INVALID;
+    // Rows are staged with 16-byte loads and outputs stored as 16-byte pairs.
+    if (((uintptr_t)d_mat | (uintptr_t)d_out) & 15) return ZKIE_ERR_INVALID;
     if (h == 0) return ZKIE_OK;
     const std::vector<uint64_t> eq = eq_table(r, k);
     const unsigned grid = (unsigned)((h + 255) / 256);
@@ -230,12 +232,16 @@ int fold_rows_at_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ex
     for (uint64_t i = 0; i < n; i++)
         if (ids[i] >= h) return ZKIE_ERR_INVALID;
     const uint64_t width = (is_ext ? 2ull : 1ull) << k;
-    Scratch ws(WS_FOLD, (n + n * width + 2 * n) * 8, s);
+    // ids | rows | out, each region starting on a 256-byte boundary (the
+    // fold stages rows with 16-byte loads and stores 16-byte outputs).
+    auto round256 = [](uint64_t words) { return (words + 31) / 32 * 32; };
+    const uint64_t ids_words = round256(n), rows_words = round256(n * width);
+    Scratch ws(WS_FOLD, (ids_words + rows_words + 2 * n) * 8, s);
     if (ws.status()) return ws.status();
     uint64_t* buf = (uint64_t*)ws.get();
     uint64_t* d_ids = buf;
-    uint64_t* d_rows = buf + n;
-    uint64_t* d_out = d_rows + n * width;
+    uint64_t* d_rows = buf + ids_words;
+    uint64_t* d_out = d_rows + rows_words;
     ZK_TRY(hipMemcpyAsync(d_ids, ids, n * 8, hipMemcpyHostToDevice, s));
     gather_rows_kernel<<<(unsigned)((n * width + 255) / 256), 256, 0, s>>>(d_mat, width, d_ids, n, d_rows);
     ZK_LAUNCHED();

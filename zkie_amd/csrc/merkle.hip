@@ -308,6 +308,8 @@ int launch_leaves(const uint64_t* mat, uint64_t* dig, uint64_t r0, uint64_t r1, 
                   bool fast, hipStream_t s)
 {
     if (r1 <= r0) return ZKIE_OK;
+    // Even-width rows are read with 16-byte loads; digests are stored as 16-byte pairs.
+    if (((uintptr_t)dig & 15) || ((w % 2) == 0 && ((uintptr_t)mat & 15))) return ZKIE_ERR_INVALID;
     const unsigned grid = grid_for(r1 - r0);
     ProfMark m = prof_begin("p2_leaf", s);
 #define ZK_LEAF(WW)                                                                                   \
@@ -341,6 +343,7 @@ int launch_compress(const uint64_t* prev, uint64_t* next, uint64_t from, uint64_
                     uint64_t pad_to, uint32_t step, bool fast, hipStream_t s)
 {
     if (pad_to <= from) return ZKIE_OK;
+    if (((uintptr_t)prev | (uintptr_t)next) & 15) return ZKIE_ERR_INVALID;  // 16-byte digest loads and stores
     ProfMark m = prof_begin("p2_compress", s);
     if (pad_to - from <= kX16MaxParents)
         compress_x16_kernel<<<grid_for((pad_to - from) * 16), 256, 0, s>>>(prev, next, from, to, pad_to, step);

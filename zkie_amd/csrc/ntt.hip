@@ -26,7 +26,12 @@ namespace zk {
 namespace {
 
 constexpr int kMaxDevices = 64;
-uint64_t* g_tables[kMaxDevices];
+
+// The twiddle tables live in device memory of the code object itself (one
+// copy per device, held until the process ends), filled from the host on
+// the first transform on each device: no allocation after that first call.
+__device__ __align__(256) uint64_t g_twiddles[kTableLen];
+const uint64_t* g_tables[kMaxDevices];
 std::mutex g_tab_mu;
 
 int ensure_tables(const uint64_t** out)
@@ -37,9 +42,9 @@ int ensure_tables(const uint64_t** out)
     if (!g_tables[dev]) {
         const std::vector<uint64_t> h = build_twiddle_tables();
         void* d = nullptr;
-        ZK_TRY(hipMalloc(&d, h.size() * 8));
+        ZK_TRY(hipGetSymbolAddress(&d, HIP_SYMBOL(g_twiddles)));
         ZK_TRY(hipMemcpy(d, h.data(), h.size() * 8, hipMemcpyHostToDevice));
-        g_tables[dev] = (uint64_t*)d;
+        g_tables[dev] = (const uint64_t*)d;
     }
     *out = g_tables[dev];
     return ZKIE_OK;
@@ -95,12 +100,21 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
 template <int S, int KNZ, bool INV, int ROLE, int LOGV, int ROWS>
 hipError_t launch_one(const PassArgs& a, uint64_t blocks, size_t shmem, hipStream_t s)
 {
-    static size_t raised = 64 * 1024;
-    if (shmem > raised) {
-        hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV, ROWS>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
-        if (e != hipSuccess) return e;
-        raised = shmem;
+    // The raised limit is kept per device (the attribute is set with that
+    // device current) and under a lock, so concurrent callers never record a
+    // limit larger than the one actually set.
+    static std::mutex mu;
+    static size_t raised[kMaxDevices];
+    if (shmem > 64 * 1024) {
+        const int dev = current_device();
+        if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+        std::lock_guard<std::mutex> g(mu);
+        if (shmem > raised[dev]) {
+            hipError_t e = hipFuncSetAttribute((const void*)&ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV, ROWS>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+            if (e != hipSuccess) return e;
+            raised[dev] = shmem;
+        }
     }
     dim3 grid;
     if (blocks <= 0x7FFFFFFFull) {
@@ -184,17 +198,37 @@ hipError_t launch_pass(const PassArgs& a, int knz, uint64_t blocks, size_t shmem
     }
 }
 
+// Grid of a grid-stride launch over n items (256 threads per workgroup).
+unsigned stride_grid(uint64_t n)
+{
+    const uint64_t g = (n + 255) / 256;
+    return (unsigned)(g < (1ull << 20) ? (g ? g : 1) : (1ull << 20));
+}
+
+// Powers of the coset shift, formed on the device: lo[k] = shift^k and
+// hi[k] = shift^(k 2^16) for k < 2^16, so shift^j = lo[j mod 2^16] hi[j >> 16].
+__global__ __launch_bounds__(256) void coset_tables_kernel(uint64_t shift, uint64_t* __restrict__ lo,
+                                                           uint64_t* __restrict__ hi)
+{
+    const uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= kBigLen) return;
+    lo[k] = gl_pow(shift, k);
+    hi[k] = gl_pow(shift, k << 16);
+}
+
 // Multiply row j of an h x w matrix by shift^j, shift^j = lo[j & 0xFFFF] * hi[j >> 16].
 __global__ __launch_bounds__(256) void coset_scale_kernel(const uint64_t* __restrict__ in,
                                                           uint64_t* __restrict__ out, uint64_t h,
                                                           uint64_t w, const uint64_t* __restrict__ lo,
                                                           const uint64_t* __restrict__ hi)
 {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= h * w) return;
-    const uint64_t j = t / w;
-    const uint64_t sj = gl_mul(lo[j & 0xFFFF], hi[j >> 16]);
-    out[t] = gl_mul(in[t], sj);
+    const uint64_t total = h * w;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t j = t / w;
+        const uint64_t sj = gl_mul(lo[j & 0xFFFF], hi[j >> 16]);
+        out[t] = gl_canon(gl_mul(in[t], sj));
+    }
 }
 
 // Run all passes (see pass_args for the buffer roles).
@@ -234,9 +268,8 @@ int dft_inplace(uint64_t* d_mat, uint64_t* d_tmp, uint32_t lg, uint64_t w, bool 
 
 }  // namespace
 
-// Exposed to the other translation units of the library.
-int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
-               uint64_t* d_out, hipStream_t s)
+int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws)
 {
     if (h == 0 || (h & (h - 1)) != 0 || !d_in || !d_out) return ZKIE_ERR_INVALID;
     uint32_t lgh = 0;
@@ -247,31 +280,29 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
     const uint64_t n = 1ull << L;
     const Plan p = make_plan(L, w);
     if (!plan_fits(p, w)) return ZKIE_ERR_INVALID;
+    if (ws && p.np > 1 && n * w > ws->ntt_words) return ZKIE_ERR_INVALID;
     const uint64_t* src = d_in;
     shift = gl_canon(shift);
     if (shift != 1) {
-        // coset: x_j <- x_j shift^j, staged in the head of d_out.
-        std::vector<uint64_t> tab(2 * kBigLen);
-        uint64_t x = 1;
-        for (uint64_t k = 0; k < kBigLen; k++) {
-            tab[k] = x;
-            x = gl_canon(gl_mul(x, shift));
+        // coset: x_j <- x_j shift^j, staged in the head of d_out. The powers
+        // are formed on the device on the call's stream, so nothing waits
+        // for the host.
+        auto scale = [&](uint64_t* d_tab) -> int {
+            coset_tables_kernel<<<(unsigned)(kBigLen / 256), 256, 0, s>>>(shift, d_tab, d_tab + kBigLen);
+            ZK_LAUNCHED();
+            coset_scale_kernel<<<stride_grid(h * w), 256, 0, s>>>(d_in, d_out, h, w, d_tab, d_tab + kBigLen);
+            ZK_LAUNCHED();
+            return ZKIE_OK;
+        };
+        int rc;
+        if (ws) {
+            rc = scale(ws->coset);
+        } else {
+            Scratch lease(WS_MISC, 2 * kBigLen * 8, s);  // released before the WS_NTT lease below
+            if (lease.status()) return lease.status();
+            rc = scale((uint64_t*)lease.get());
         }
-        const uint64_t step = x;
-        x = 1;
-        for (uint64_t k = 0; k < kBigLen; k++) {
-            tab[kBigLen + k] = x;
-            x = gl_canon(gl_mul(x, step));
-        }
-        Scratch ws(WS_MISC, tab.size() * 8, s);  // released before the WS_NTT lease below
-        if (ws.status()) return ws.status();
-        uint64_t* d_tab = (uint64_t*)ws.get();
-        ZK_TRY(hipMemcpyAsync(d_tab, tab.data(), tab.size() * 8, hipMemcpyHostToDevice, s));
-        const uint64_t total = h * w;
-        coset_scale_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(d_in, d_out, h, w, d_tab,
-                                                                          d_tab + kBigLen);
-        ZK_LAUNCHED();
-        ZK_TRY(hipStreamSynchronize(s));  // the table was copied from a host vector
+        if (rc) return rc;
         src = d_out;
     }
     if (p.np == 1) {
@@ -281,22 +312,32 @@ int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup
         }
         return run_passes(p, w, src, h, nullptr, d_out, false, s);
     }
-    Scratch ws(WS_NTT, n * w * 8, s);
-    if (ws.status()) return ws.status();
-    return run_passes(p, w, src, h, (uint64_t*)ws.get(), d_out, false, s);
+    if (ws) return run_passes(p, w, src, h, ws->ntt, d_out, false, s);
+    Scratch lease(WS_NTT, n * w * 8, s);
+    if (lease.status()) return lease.status();
+    return run_passes(p, w, src, h, (uint64_t*)lease.get(), d_out, false, s);
+}
+
+// Exposed to the other translation units of the library.
+int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+               uint64_t* d_out, hipStream_t s)
+{
+    return lde_run(d_in, h, w, log_blowup, shift, d_out, s, nullptr);
 }
 
 // Prefix order (writer.rs:43-71): entry (i, j) of the committed matrix, row
 // i < 2^lrows and column j < 2^k, is poly[j 2^lrows + i]; E u64 per entry.
+// `total` = E 2^(lrows + k) u64 (up to 2^33 for a 32-variable EF table).
 __global__ __launch_bounds__(256) void prefix_transpose_kernel(const uint64_t* __restrict__ in,
-                                                               uint64_t* __restrict__ out, uint32_t lrows,
-                                                               uint32_t k, uint32_t E)
+                                                               uint64_t* __restrict__ out, uint64_t total,
+                                                               uint32_t lrows, uint32_t k, uint32_t E)
 {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (E << (lrows + k))) return;
-    const uint64_t c = t % E, e = t / E;
-    const uint64_t j = e & ((1ull << k) - 1), i = e >> k;
-    out[t] = in[((j << lrows) | i) * E + c];
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t c = t % E, e = t / E;
+        const uint64_t j = e & ((1ull << k) - 1), i = e >> k;
+        out[t] = in[((j << lrows) | i) * E + c];
+    }
 }
 
 // commit_extension's encoding (writer.rs:21-86): the 2^n-entry table as a
@@ -312,8 +353,8 @@ int whir_encode_device(const uint64_t* d_poly, uint32_t n_vars, int is_ext, uint
     if (!prefix) return lde_device(d_poly, h, w, log_inv_rate, 1, d_out, s);
     const uint64_t total = h * w;
     if (d_poly < d_out + total && d_out < d_poly + total) return ZKIE_ERR_INVALID;  // no in-place transpose
-    prefix_transpose_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(d_poly, d_out, n_vars - k, k,
-                                                                          (uint32_t)E);
+    prefix_transpose_kernel<<<stride_grid(total), 256, 0, s>>>(d_poly, d_out, total, n_vars - k, k,
+                                                               (uint32_t)E);
     ZK_LAUNCHED();
     return lde_device(d_out, h, w, log_inv_rate, 1, d_out, s);
 }

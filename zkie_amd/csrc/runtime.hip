@@ -144,28 +144,32 @@ Scratch::~Scratch()
 ProfMark prof_begin(const char* kernel, hipStream_t s)
 {
     ProfState& P = prof();
-    std::lock_guard<std::mutex> g(P.mu);
     ProfMark m;
-    if (!P.on) return m;
-    ProfRecord r;
-    r.kernel = prof_id(P, kernel);
-    if (hipEventCreate(&r.a) != hipSuccess) return m;
-    if (hipEventCreate(&r.b) != hipSuccess) {
-        (void)hipEventDestroy(r.a);
+    {
+        std::lock_guard<std::mutex> g(P.mu);
+        if (!P.on) return m;
+        m.kernel = prof_id(P, kernel);
+    }
+    if (hipEventCreate(&m.a) != hipSuccess) {
+        m.kernel = -1;
         return m;
     }
-    (void)hipEventRecord(r.a, s);
-    P.pending.push_back(r);
-    m.id = (int)P.pending.size() - 1;
+    if (hipEventCreate(&m.b) != hipSuccess) {
+        (void)hipEventDestroy(m.a);
+        m.kernel = -1;
+        return m;
+    }
+    (void)hipEventRecord(m.a, s);
     return m;
 }
 
 void prof_end(ProfMark m, hipStream_t s)
 {
-    if (m.id < 0) return;
+    if (m.kernel < 0) return;
+    (void)hipEventRecord(m.b, s);
     ProfState& P = prof();
     std::lock_guard<std::mutex> g(P.mu);
-    if (m.id < (int)P.pending.size()) (void)hipEventRecord(P.pending[m.id].b, s);
+    P.pending.push_back(ProfRecord{m.kernel, m.a, m.b});
 }
 
 }  // namespace zk

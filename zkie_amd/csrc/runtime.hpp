@@ -59,14 +59,30 @@ private:
 };
 
 // Kernel timers: when profiling is on, every instrumented launch records a
-// HIP event pair on the launch stream; totals are read back on query.
+// HIP event pair on the launch stream; totals are read back on query. A mark
+// owns its event pair until prof_end hands it to the pending list, so a
+// concurrent drain never touches a pair whose end is not recorded yet.
 struct ProfMark {
-    int id = -1;
+    int kernel = -1;
+    hipEvent_t a = nullptr, b = nullptr;
 };
 ProfMark prof_begin(const char* kernel, hipStream_t s);
 void prof_end(ProfMark m, hipStream_t s);
 
 // Current device ordinal (for per-device caches).
 int current_device();
+
+// Work buffers of an LDE supplied by the caller instead of leased from the
+// library's scratch: `ntt` holds the intermediate of a multi-pass transform
+// (ntt_words u64), `coset` the 2 x 2^16 powers of a coset shift.
+struct LdeWorkspace {
+    uint64_t* ntt = nullptr;
+    uint64_t ntt_words = 0;
+    uint64_t* coset = nullptr;
+};
+
+// zkie_lde_batch with the work buffers of `ws`, or leased ones when ws is null.
+int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws);
 
 }  // namespace zk
