@@ -33,6 +33,7 @@ extern "C" {
 #define ZKIE_ERR_NO_DEVICE (-2)   /* no HIP device */
 #define ZKIE_ERR_ALLOC (-3)       /* device workspace allocation failed */
 #define ZKIE_ERR_IO (-4)          /* a caller's write or read callback failed */
+#define ZKIE_ERR_SCRATCH_LIMIT (-5) /* larger than a no-alloc entry point's fixed scratch */
 
 /* ------------------------------------------------------------------------
  * Device and memory. Replace the raw CUDA runtime imports of
@@ -115,6 +116,20 @@ int zkie_idft_batch(uint64_t *d_mat, uint32_t lg_h, uint64_t w, void *stream);
  * d_out. h must be a power of two. d_in and d_out must not overlap. */
 int zkie_lde_batch(const uint64_t *d_in, uint64_t h, uint64_t w, uint32_t log_blowup,
                    uint64_t shift, uint64_t *d_out, void *stream);
+
+/* No counterpart in the reference. zkie_lde_batch for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. Same arguments, semantics and results as
+ * zkie_lde_batch; its work buffers live in a fixed array in device memory of
+ * the library (64 MiB plus 1 MiB per device that loads it, held until the
+ * process ends) instead of being allocated, so it calls no hipMalloc or
+ * hipFree. The first call on a device (with that device current) looks up the
+ * array and fills the twiddle tables. Sizes with (h << log_blowup) * w above
+ * 2^23 u64 return ZKIE_ERR_SCRATCH_LIMIT. All calls on one device share the
+ * array: calls that overlap on one device (unordered streams, or host
+ * threads) race; order them. */
+int zkie_lde_batch_noalloc(const uint64_t *d_in, uint64_t h, uint64_t w, uint32_t log_blowup,
+                           uint64_t shift, uint64_t *d_out, void *stream);
 
 /* Tree geometry of MerkleTree::new for one matrix of height h, arity 2
  * (p3-merkle-tree merkle_tree.rs:95-178, padded_len at :577-585; the same

@@ -42,6 +42,7 @@ SIGNATURES = {
     "zkie_dft_batch": [_vp, _u32, _u64, _vp],
     "zkie_idft_batch": [_vp, _u32, _u64, _vp],
     "zkie_lde_batch": [_vp, _u64, _u64, _u32, _u64, _vp, _vp],
+    "zkie_lde_batch_noalloc": [_vp, _u64, _u64, _u32, _u64, _vp, _vp],
     "zkie_merkle_layout": [_u64, _u32p, _u64p],
     "zkie_merkle_commit": [_vp, _u64, _u64, _vp, _u64p, _vp],
     "zkie_merkle_open_batch": [_vp, _u64, _u64, _vp, _u64p, _u64, _u64p, _u64p, _vp],

@@ -18,7 +18,8 @@ LIB = os.path.join(HERE, "libzkie_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("ZKIE_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["runtime.hip", "ntt.hip", "merkle.hip", "fold.hip", "sumcheck.hip", "prover_data.hip"]
+SOURCES = ["runtime.hip", "ntt.hip", "merkle.hip", "fold.hip", "sumcheck.hip", "prover_data.hip",
+           "noalloc.hip"]
 
 # Packed FP32 instructions are kept out of every code object.
 COMMON = [
