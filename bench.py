@@ -1,19 +1,40 @@
 #!/usr/bin/env python3
 """Benchmark of the shard commitment hot path on one MI355X.
 
-One step = one commitment of the resident input: coset/subgroup LDE (blowup
-4), the Poseidon2 Merkle tree over the codeword rows (root read back), and
-one fold round (k = 4) over the codeword, on 2^24 rows x 16 columns of
-uniform Goldilocks elements (2^28 input elements). Prints one JSON line.
+One step = one commitment of the resident input: the LDE (blowup 4), the
+Poseidon2 Merkle tree over the codeword rows (root read back), and one fold
+round (k = 4) over the codeword, on 2^24 rows x 16 columns of uniform
+Goldilocks elements (2^28 input elements). Prints one JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config N]
-                  [--no-cpu-baseline] [--prover-data]
+                  [--no-cpu-baseline] [--prover-data] [--sumcheck]
+  python bench.py --valu-peak           # VALU issue rates per instruction kind
+  python bench.py --ingest-counters DIR # rocprofv3 counter CSVs -> profile JSON
+
+Rooflines. The step is bound by VALU issue (Poseidon2), not by HBM, so every
+roofline is given with both components:
+  * HBM: algorithmic bytes (the per-element figures below) over the measured
+    time, against 8 TB/s;
+  * VALU: VALU wave-instructions (rocprofv3 SQ_INSTS_VALU per launch, from the
+    committed counter profile, used only while its source hash matches the
+    kernel sources) over the measured time, against the issue peak measured
+    live in the same run by the probe kernels of libzkie_valu_probe.so;
+  * `bound` names the larger of the two bounds, t_hbm = bytes / 8 TB/s and
+    t_valu = instructions / issue peak, and `frac` = t_bound / t_measured.
+Algorithmic bytes per input element at the 2^24 x 16 workload: LDE 8 in +
+32 codeword out = 40; Merkle 32 (2^27 digests of 64 B written); fold 32
+codeword in + 4 out = 36; the step (fused minimum) 108.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
+import hashlib
 import json
 import os
+import platform
+import subprocess
 import sys
 import time
 
@@ -21,7 +42,27 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+CLOCK_HZ = 2.4e9               # MI355X peak engine clock
+CUS = 256
 METRIC = "committed Goldilocks elems/sec (LDE+Merkle) at 2^24x16, % HBM roofline"
+COUNTERS_JSON = os.path.join(ROOT, "profiles", "commit_step_counters.json")
+
+# Profiler names of the library's kernels and the stage each belongs to.
+STAGE_KERNELS = {
+    "lde": ("ntt_pass_first", "ntt_pass_mid", "ntt_pass_last", "ntt_last_leaf"),
+    "merkle": ("p2_leaf", "p2_compress", "p2_subtree"),
+    "fold": ("fold_rows",),
+}
+
+# VALU probe kinds (zkie_amd/csrc/valu_probe.hip).
+PROBE_KINDS = ["v_add_u32 (VOP2)", "v_add_co_u32 (VOP3, SGPR carry)", "v_mad_u64_u32",
+               "v_mul_lo_u32", "v_addc_co_u32 (VOP3)", "v_cndmask_b32 (VOP3)",
+               "field-product mix (6 mad, 1 cndmask, 2 subb, 3 mov, 4 add)",
+               "v_add_u32_e64 (VOP3 encoding)", "v_add_co_u32_e32 (VOP2, VCC)",
+               "64-bit add on VCC (add_co, 2 add, addc; VOP2)", "v_cndmask_b32_e32 (VOP2, VCC)", "v_mov_b32 (VOP1)",
+               "v_mov_b64 (VOP1)", "v_lshl_add_u64 (VOP3)", "v_add_u32 + literal", "v_add_u32 / s_nop 0",
+               "v_xor_b32 (VOP2)", "v_add3_u32 (VOP3)", "v_lshlrev_b32 (VOP2)",
+               "64-bit sub on VCC (sub_co, s_nop 1, subb; VOP2)"]
 
 
 def parse():
@@ -43,7 +84,104 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after the run, copy MIB MiB device to device three times (a plain "
                          "copy kernel of known size for scaling rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--valu-peak", action="store_true",
+                    help="only run the VALU issue-rate probe (every kind) and print its JSON")
+    ap.add_argument("--probe-ms", type=float, default=60.0,
+                    help="approximate duration of each probe launch")
+    ap.add_argument("--ingest-counters", metavar="DIR",
+                    help="read rocprofv3 --pmc CSVs under DIR (subfolders fetch, write, valu) of a "
+                         "'bench.py --steps 1 --warmup 1 --no-cpu-baseline --copy-calibration 1024' "
+                         "run and write profiles/commit_step_counters.json")
     return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# Kernel sources and the counter profile measured on them.
+
+def source_hash() -> str:
+    """Hash of the kernel sources: a counter profile is valid only for the
+    code it was measured on."""
+    h = hashlib.sha256()
+    for path in sorted(glob.glob(os.path.join(ROOT, "zkie_amd", "csrc", "*"))):
+        if path.endswith((".hip", ".hpp")) and not path.endswith("valu_probe.hip"):
+            h.update(os.path.basename(path).encode())
+            with open(path, "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def load_counters():
+    """The committed per-launch counters, or (None, reason) when missing or
+    measured on other kernel sources."""
+    if not os.path.exists(COUNTERS_JSON):
+        return None, "no counter profile"
+    with open(COUNTERS_JSON) as f:
+        prof = json.load(f)
+    if prof.get("source_hash") != source_hash():
+        return None, (f"counter profile measured on sources {prof.get('source_hash')}, "
+                      f"kernels now {source_hash()}: stale, not used")
+    return prof, None
+
+
+# ---------------------------------------------------------------------------
+# VALU issue-rate probe.
+
+def probe_lib():
+    import ctypes
+
+    path = os.path.join(ROOT, "zkie_amd", "libzkie_valu_probe.so")
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build with python -m zkie_amd.build")
+    L = ctypes.CDLL(path)
+    L.zkie_valu_probe_run.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)]
+    L.zkie_valu_probe_run.restype = ctypes.c_int
+    return L
+
+
+def valu_probe(kinds, target_ms: float = 60.0):
+    """Issue rate of each probe kind: 8192 workgroups of 256 threads (8 waves
+    per SIMD on every CU, four times over), iterations scaled so a launch
+    takes about target_ms; the best of three launches."""
+    import ctypes
+
+    from zkie_amd import _native as N
+
+    L = probe_lib()
+    blocks = 8192
+    out = N.DeviceBuffer(blocks * 256 // 2)
+    res = {}
+    for kind in kinds:
+        ms, wi = ctypes.c_double(), ctypes.c_uint64()
+        iters = 256
+        N.check(L.zkie_valu_probe_run(kind, blocks, iters, out.addr, ctypes.byref(ms), ctypes.byref(wi)),
+                "valu probe")
+        iters = min(1 << 22, max(256, int(iters * target_ms / max(ms.value, 1e-3))))
+        best = None
+        for _ in range(3):
+            N.check(L.zkie_valu_probe_run(kind, blocks, iters, out.addr, ctypes.byref(ms), ctypes.byref(wi)),
+                    "valu probe")
+            rate = wi.value / (ms.value * 1e-3)
+            if best is None or rate > best[0]:
+                best = (rate, ms.value, wi.value)
+        rate, t, w = best
+        res[kind] = {"kind": PROBE_KINDS[kind], "wave_instr": w, "ms": round(t, 3),
+                     "wave_instr_per_s": rate, "per_cu_per_clock": rate / CUS / CLOCK_HZ}
+    return res
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline.
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(wl, rows: int, threads: int = 0):
@@ -69,16 +207,14 @@ def cpu_baseline(wl, rows: int, threads: int = 0):
         "unit": "elem/s",
         "cores": threads,
         "kind": "port",
+        "cpu": cpu_model(),
         "sample": f"{sample.rows} rows x {sample.cols} cols, blowup {1 << sample.log_blowup}, "
                   f"LDE + Merkle root + fold k={wl.fold_k}; {dt:.2f} s wall",
     }
 
 
-# Issue peak of the VALU: 256 CUs x 2.4 GHz x 1.35 wave-instructions per CU
-# per clock, the fastest rate measured on gfx950 (plain 32-bit VOP1/VOP2 ops;
-# v_mad_u64_u32 and other VOP3 forms issue at about 0.86-0.93).
-VALU_PEAK_WINSTR_S = 256 * 2.4e9 * 1.35
-
+# ---------------------------------------------------------------------------
+# Extra measurements.
 
 def prover_data_stream(N, d_cw, n: int, w: int, d_layers, stream, reps: int = 2):
     """Time zkie_prover_data_write of the step's tree (matrix + digest layers,
@@ -152,15 +288,36 @@ def h2d_seconds(N, d_in, data, reps: int = 2) -> float:
     return (time.perf_counter() - t0) / reps
 
 
-def leaf_profile():
-    """Per-launch figures of the leaf kernel measured with rocprofv3 at this
-    workload: HBM bytes (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled) and VALU
-    wave-instructions, from the committed profile summaries."""
-    path = os.path.join(ROOT, "profiles", "p2_leaf_traffic.json")
-    if not os.path.exists(path):
-        return {}
-    with open(path) as f:
-        return json.load(f)
+# ---------------------------------------------------------------------------
+# Rooflines.
+
+def alg_bytes(wl, lens):
+    """Algorithmic HBM bytes of each stage: the LDE reads the input and
+    writes the codeword; the Merkle tree writes every digest once (the
+    codeword read is shared with the LDE's write in the fused minimum); the
+    fold reads the codeword and writes one EF element per row."""
+    n, w = wl.codeword_rows, wl.cols
+    out = {"lde": wl.elems * 8 + n * w * 8, "merkle": sum(lens) * 64}
+    if wl.fold_k:
+        out["fold"] = n * w * 8 + n * 16
+    return out
+
+
+def roofline(t_s: float, nbytes: float, valu_instr, valu_peak: float, traffic=None):
+    """Both bounds of a kernel or stage taking t_s seconds."""
+    hbm = {"achieved": nbytes / t_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": nbytes / t_s / 1e9 / HBM_PEAK_GBS, "alg_bytes": nbytes, "traffic": traffic,
+           "t_bound_ms": nbytes / (HBM_PEAK_GBS * 1e9) * 1e3}
+    r = {"hbm": hbm, "valu": None, "bound": "hbm", "t_bound_ms": hbm["t_bound_ms"], "ms": t_s * 1e3,
+         "frac": hbm["frac"]}
+    if valu_instr:
+        v = {"achieved": valu_instr / t_s, "peak": valu_peak, "unit": "wave-instr/s",
+             "frac": valu_instr / t_s / valu_peak, "wave_instr": valu_instr,
+             "t_bound_ms": valu_instr / valu_peak * 1e3}
+        r["valu"] = v
+        if v["t_bound_ms"] > hbm["t_bound_ms"]:
+            r.update(bound="valu", t_bound_ms=v["t_bound_ms"], frac=v["frac"])
+    return r
 
 
 def main():
@@ -169,10 +326,17 @@ def main():
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the multi-GPU "
               "sharding of this path is a design, not a measured configuration.", file=sys.stderr)
         sys.exit(2)
+    if args.ingest_counters:
+        ingest_counters(args.ingest_counters)
+        return
+    if args.valu_peak:
+        res = valu_probe(range(len(PROBE_KINDS)), args.probe_ms)
+        print(json.dumps({"valu_issue_rates": list(res.values()), "cus": CUS, "clock_hz": CLOCK_HZ}), flush=True)
+        return
 
     from zkie_amd import _native as N
     from zkie_amd import configs as C
-    from zkie_amd.pcs import HipMerkleTreeMmcs, fold_rows_device, lde_device
+    from zkie_amd.pcs import fold_rows_device, lde_device
     from zkie_amd._native import DeviceBuffer
 
     wl = C.CONFIGS[args.config]
@@ -185,7 +349,6 @@ def main():
     d_layers = DeviceBuffer(sum(lens) * 8)
     d_fold = DeviceBuffer(2 * n) if wl.fold_k else None
     ch = C.challenges(wl.fold_k) if wl.fold_k else None
-    mmcs = HipMerkleTreeMmcs()
     L = N.load()
     import numpy as np
     root = np.zeros(8, np.uint64)
@@ -212,40 +375,62 @@ def main():
     h2d_s = h2d_seconds(N, d_in, data)
     del data
 
-    value = wl.elems / t
-    # Dominant kernel: the Merkle leaf hash (2 of the 3 permutations per row).
-    leaf_n, leaf_ms = per_kernel.get("p2_leaf", (0, 0.0))
-    leaf_avg_ms = leaf_ms / max(leaf_n, 1)
-    leaf_alg_bytes = n * w * 8 + n * 64       # read the codeword rows, write layer-0 digests
-    achieved = leaf_alg_bytes / (leaf_avg_ms * 1e-3) / 1e9 if leaf_avg_ms else 0.0
-    prof = leaf_profile() if args.config == 3 else {}
-    traffic = prof.get("bytes_per_launch")
-    stage_ms = {k: round(ms / max(cnt, 1) * max(cnt, 1) / args.steps, 3) for k, (cnt, ms) in per_kernel.items()}
-    # whole-step HBM floor: 8 B in + 32 B codeword + 32 B digests (+ 36 B fold) per input element
-    step_alg_bytes = wl.elems * (72 + (36 if wl.fold_k else 0))
-    # Per stage: time per step and its algorithmic HBM bytes at the 8 TB/s peak.
-    # LDE: every pass reads and writes the codeword (the first reads the input);
-    # Merkle: rows in, every digest layer written once and read once;
-    # fold: codeword in, one EF element per row out.
-    lg_n = n.bit_length() - 1
-    passes = (lg_n + 8) // 9
-    lde_bytes = wl.elems * 8 + n * w * 8 * (2 * passes - 1)
-    merkle_bytes = n * w * 8 + 2 * (2 * n) * 64
-    fold_bytes = n * w * 8 + n * 16 if wl.fold_k else 0
+    # Issue peak of the VALU, measured now: the fastest of the plain 32-bit
+    # operations (v_add_u32 in both encodings, v_mov_b32) and, for reference,
+    # the mix of the field product the Poseidon2 kernels run.
+    probe = valu_probe([0, 7, 11, 6], args.probe_ms)
+    valu_peak = max(p["wave_instr_per_s"] for p in probe.values())
 
-    def stage(names, alg):
-        ms = sum(per_kernel.get(k, (0, 0.0))[1] for k in names) / args.steps
-        return {"ms": round(ms, 3), "alg_bytes": alg,
-                "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if ms else None}
+    counters, stale = load_counters() if args.config == 3 else (None, "counters are profiled at configuration 3")
+    kc = (counters or {}).get("kernels", {})
 
-    stages = {"lde": stage([k for k in per_kernel if k.startswith("ntt_pass")], lde_bytes),
-              "merkle": stage(["p2_leaf", "p2_compress", "p2_subtree"], merkle_bytes)}
-    if wl.fold_k:
-        stages["fold"] = stage(["fold_rows"], fold_bytes)
+    def per_step(name, field):
+        """A kernel's counter summed over one step (None without a valid profile)."""
+        return kc.get(name, {}).get(field + "_per_step")
+
+    ab = alg_bytes(wl, lens)
+    step_ms = {k: ms / args.steps for k, (cnt, ms) in per_kernel.items()}
+    # Dominant kernel: the Merkle leaf hash (or the fused last NTT pass + leaf hash).
+    dom = "ntt_last_leaf" if "ntt_last_leaf" in per_kernel else "p2_leaf"
+    dn, dms = per_kernel.get(dom, (0, 0.0))
+    dom_avg_s = dms / max(dn, 1) * 1e-3
+    # Its algorithmic bytes per launch: read the rows (or, fused, the last
+    # pass's input) and write the layer-0 digests (and, fused, the codeword).
+    dom_bytes = n * w * 8 + n * 64 + (n * w * 8 if dom == "ntt_last_leaf" else 0)
+    dom_launches = dn / args.steps
+    dom_traffic = dom_valu = None
+    if per_step(dom, "fetch_bytes") is not None:
+        dom_traffic = (per_step(dom, "fetch_bytes") + per_step(dom, "write_bytes")) / dom_launches
+        dom_valu = per_step(dom, "valu_wave_instr") / dom_launches
+    dom_roof = roofline(dom_avg_s, dom_bytes, dom_valu, valu_peak, dom_traffic)
+
+    stages = {}
+    for st, names in STAGE_KERNELS.items():
+        if st not in ab:
+            continue
+        ms = sum(step_ms.get(k, 0.0) for k in names)
+        if not ms:
+            continue
+        vi = tr = None
+        if counters:
+            vi = sum(per_step(k, "valu_wave_instr") or 0 for k in names if k in per_kernel)
+            tr = sum((per_step(k, "fetch_bytes") or 0) + (per_step(k, "write_bytes") or 0)
+                     for k in names if k in per_kernel)
+        stages[st] = roofline(ms * 1e-3, ab[st], vi, valu_peak, tr)
+    step_bytes = sum(ab.values())
+    step_valu = sum(s["valu"]["wave_instr"] for s in stages.values() if s["valu"]) if counters else None
+    step_roof = roofline(t, step_bytes, step_valu, valu_peak)
+
+    def headline(r, kernel):
+        """The contract's roofline object for the binding component."""
+        c = r[r["bound"]]
+        return {"bound": r["bound"], "kernel": kernel, "achieved": c["achieved"], "peak": c["peak"],
+                "unit": c["unit"], "frac": c["frac"], "traffic": r["hbm"]["traffic"],
+                "avg_ms": r["ms"], "hbm": r["hbm"], "valu": r["valu"]}
 
     out = {
         "metric": METRIC,
-        "value": value,
+        "value": wl.elems / t,
         "unit": "elem/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -259,18 +444,15 @@ def main():
         "config": {"workload": wl.name, "rows": wl.rows, "cols": wl.cols,
                    "log_blowup": wl.log_blowup, "fold_k": wl.fold_k,
                    "codeword_rows": n, "parallelism": "single-gpu"},
-        "roofline": {"bound": "hbm", "kernel": "p2_leaf", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic, "avg_ms": leaf_avg_ms},
-        "step_hbm_frac": step_alg_bytes / t / 1e9 / HBM_PEAK_GBS,
-        # The leaf kernel is bound by VALU issue, not HBM: its rocprof VALU count
-        # over its live duration against the issue peak.
-        "valu_roofline": ({"kernel": "p2_leaf", "achieved": prof["valu_per_launch"] / (leaf_avg_ms * 1e-3),
-                           "peak": VALU_PEAK_WINSTR_S, "unit": "wave-instr/s",
-                           "frac": prof["valu_per_launch"] / (leaf_avg_ms * 1e-3) / VALU_PEAK_WINSTR_S}
-                          if prof.get("valu_per_launch") and leaf_avg_ms else None),
-        "stage_ms_per_step": stage_ms,
+        "roofline": headline(dom_roof, dom),
+        "step_roofline": headline(step_roof, "step"),
+        "step_hbm_frac": step_roof["hbm"]["frac"],
         "stages": stages,
+        "stage_ms_per_step": {k: round(v, 3) for k, v in step_ms.items()},
+        "valu_peak": {"wave_instr_per_s": valu_peak, "probe": list(probe.values()),
+                      "source": "libzkie_valu_probe.so, measured in this run"},
+        "counters": {"source": os.path.relpath(COUNTERS_JSON, ROOT), "used": counters is not None,
+                     "note": stale, "source_hash": source_hash()},
         # A caller that hands over the input in host memory (the reference's
         # dft_batch takes a host RowMajorMatrix) also pays its upload; the
         # tree stays in HBM and only the root comes back (inside the step).
@@ -296,6 +478,94 @@ def main():
             N.check(L.zkie_memcpy_dtod(dst.addr, src.addr, nbytes, None), "copy")
         N.check(L.zkie_device_synchronize(), "sync")
         print(f"copy calibration: 3 device-to-device copies of {nbytes} bytes", file=sys.stderr)
+
+
+# ---------------------------------------------------------------------------
+# Counter ingestion (rocprofv3 --pmc CSV -> profiles/commit_step_counters.json).
+
+# rocprofv3 kernel names -> the library's profiler names.
+KERNEL_NAMES = [("ntt_last_leaf_kernel", "ntt_last_leaf"), ("leaf_kernel", "p2_leaf"),
+                ("compress_x16_kernel", "p2_compress"), ("compress_kernel", "p2_compress"),
+                ("subtree_kernel", "p2_subtree"), ("fold_kernel", "fold_rows")]
+COPY_KERNEL = "copyBuffer"
+
+
+def _kernel_key(name: str, grid: int, first_grids: dict):
+    for pat, key in KERNEL_NAMES:
+        if pat in name:
+            return key
+    if "ntt_pass_kernel" in name:
+        # named by launch order afterwards (first, middle, last pass of a step)
+        return name
+    return None
+
+
+def ingest_counters(d: str):
+    """Per-launch counters of the step's kernels from three rocprofv3 runs
+    (one counter group each) of one step: FETCH_SIZE and WRITE_SIZE (KiB,
+    scaled by what they read for the 0.5 GiB dispatches of the trailing
+    device-to-device copies) and SQ_INSTS_VALU (wave-instructions)."""
+    vals = {}  # (group, dispatch) -> (kernel, grid, value)
+    for group, counter in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE"), ("valu", "SQ_INSTS_VALU")):
+        files = glob.glob(os.path.join(d, group, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            raise SystemExit(f"no counter_collection.csv under {os.path.join(d, group)}")
+        rows = {}
+        with open(files[0]) as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") != counter:
+                    continue
+                disp = int(r["Dispatch_Id"])
+                rows.setdefault(disp, [r["Kernel_Name"], int(r.get("Grid_Size", 0) or 0), 0.0])
+                rows[disp][2] += float(r["Counter_Value"])
+        vals[group] = rows
+    # Calibration from the trailing device-to-device copies: one dispatch of
+    # 1 GiB each (the largest copy dispatches of the run; smaller ones are
+    # the run's own small copies).
+    copy_bytes = 1 << 30
+
+    def scale(group):
+        c = [v for v in vals[group].values() if COPY_KERNEL in v[0]]
+        if not c:
+            raise SystemExit(f"no copy dispatch in the {group} run (run with --copy-calibration 1024)")
+        big = max(x[1] for x in c)
+        kib = sorted(x[2] for x in c if x[1] == big)[len([x for x in c if x[1] == big]) // 2]
+        return copy_bytes / kib
+
+    fs, ws_ = scale("fetch"), scale("write")
+    steps_profiled = 2  # --warmup 1 --steps 1
+    kernels = {}
+    ntt_order = []
+    for group, field, sc in (("fetch", "fetch_bytes", fs), ("write", "write_bytes", ws_),
+                             ("valu", "valu_wave_instr", 1.0)):
+        per = {}
+        for disp in sorted(vals[group]):
+            name, grid, v = vals[group][disp]
+            key = _kernel_key(name, grid, {})
+            if key is None:
+                continue
+            if "ntt_pass_kernel" in key and key not in ntt_order:
+                ntt_order.append(key)
+            per.setdefault(key, []).append(v * sc)
+        for key, vs in per.items():
+            kernels.setdefault(key, {})[field + "_per_step"] = sum(vs) / steps_profiled
+            kernels[key]["launches_per_step"] = len(vs) / steps_profiled
+    # Name the NTT passes by their order in the step.
+    names = {}
+    for i, k in enumerate(ntt_order):
+        names[k] = "ntt_pass_first" if i == 0 else ("ntt_pass_last" if i == len(ntt_order) - 1 else "ntt_pass_mid")
+    out = {}
+    for k, v in kernels.items():
+        out[names.get(k, k)] = dict(v, rocprof_name=k)
+    prof = {"source_hash": source_hash(), "workload": "uniform_2^24x16_blowup4_root_fold4",
+            "fetch_scale": fs, "write_scale": ws_,
+            "command": "rocprofv3 --pmc {FETCH_SIZE | WRITE_SIZE | SQ_INSTS_VALU} --output-format csv "
+                       "-d gpurun_out/prof/<group> -o bench -- python3 bench.py --steps 1 --warmup 1 "
+                       "--no-cpu-baseline --copy-calibration 1024",
+            "kernels": out}
+    with open(COUNTERS_JSON, "w") as f:
+        json.dump(prof, f, indent=1)
+    print(json.dumps(prof, indent=1))
 
 
 if __name__ == "__main__":

@@ -18,6 +18,10 @@ LIB = os.path.join(HERE, "libzkie_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("ZKIE_OFFLOAD_ARCH", "gfx950")
 
+# The VALU issue-rate probe of bench.py --valu-peak, a library of its own.
+PROBE_SRC = "valu_probe.hip"
+PROBE_LIB = os.path.join(HERE, "libzkie_valu_probe.so")
+
 SOURCES = ["runtime.hip", "ntt.hip", "merkle.hip", "fold.hip", "sumcheck.hip", "prover_data.hip",
            "noalloc.hip"]
 
@@ -60,8 +64,14 @@ def build(verbose: bool = False, force: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    probe_obj = _compile(PROBE_SRC, force)
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", probe_obj, "-o", PROBE_LIB + ".tmp"],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 
