@@ -48,9 +48,14 @@ METRIC = "committed Goldilocks elems/sec (LDE+Merkle) at 2^24x16, % HBM roofline
 COUNTERS_JSON = os.path.join(ROOT, "profiles", "commit_step_counters.json")
 
 # Profiler names of the library's kernels and the stage each belongs to.
+# With the last NTT pass fused with the leaf hash (ntt_last_leaf) one kernel
+# does part of both the LDE and the Merkle stage; the two are then reported
+# as one stage, lde+merkle.
 STAGE_KERNELS = {
-    "lde": ("ntt_pass_first", "ntt_pass_mid", "ntt_pass_last", "ntt_last_leaf"),
+    "lde": ("ntt_pass_first", "ntt_pass_mid", "ntt_pass_last"),
     "merkle": ("p2_leaf", "p2_compress", "p2_subtree"),
+    "lde+merkle": ("ntt_pass_first", "ntt_pass_mid", "ntt_pass_last", "ntt_last_leaf", "p2_leaf",
+                   "p2_compress", "p2_subtree"),
     "fold": ("fold_rows",),
 }
 
@@ -72,7 +77,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=1 << 20,
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="commit with separate zkie_lde_batch and zkie_merkle_commit calls (the leaf "
+                         "kernel re-reads the codeword) instead of zkie_lde_commit")
+    ap.add_argument("--cpu-rows", type=int, default=1 << 21,
                     help="coefficient rows of the CPU baseline sample")
     ap.add_argument("--prover-data", action="store_true",
                     help="after the timed steps, also time streaming the committed tree out of "
@@ -185,28 +193,35 @@ def cpu_model() -> str:
 
 
 def cpu_baseline(wl, rows: int, threads: int = 0):
-    """The oracle (C restatement of the reference CPU path) on a bounded
-    sample of the same workload, on `threads` host threads (0: all host
-    cores, at most 16, the CPU share of the machine)."""
+    """The CPU baseline (oracle/cpu_baseline.c: the reference CPU commit path
+    restated with AVX2-packed Goldilocks arithmetic and OpenMP, bit-identical
+    to the oracle) on a bounded sample of the same workload, on `threads`
+    host threads (0: the process's CPU share, OMP_NUM_THREADS when set, else
+    every core the OS shows)."""
+    from oracle import cpu_baseline as CB
     from oracle import oracle as O
     from zkie_amd import configs as C
 
-    threads = threads or min(os.cpu_count() or 1, 16)
-    O.set_threads(threads)
+    nproc = os.cpu_count() or 1
+    threads = threads or min(int(os.environ.get("OMP_NUM_THREADS") or nproc), nproc)
+    CB.set_threads(threads)
+    CB.set_constants(*O.p2_constants())
     sample = wl.scaled(rows)
     data = O.gen_uniform(C.SEED_DATA, sample.elems).reshape(sample.rows, sample.cols)
     ch = C.challenges(wl.fold_k) if wl.fold_k else None
     t0 = time.perf_counter()
-    cw = O.lde_batch(data, sample.log_blowup)
-    _, root = O.merkle_commit(cw)
+    cw = CB.lde_batch(data, sample.log_blowup)
+    _, root = CB.merkle_commit(cw)
     if ch is not None:
-        O.fold_rows(cw, wl.fold_k, ch, False)
+        CB.fold_rows(cw, wl.fold_k, ch)
     dt = time.perf_counter() - t0
     return {
         "value": sample.elems / dt,
         "unit": "elem/s",
         "cores": threads,
+        "nproc": nproc,
         "kind": "port",
+        "isa": "AVX2 (4 x u64 lanes), OpenMP",
         "cpu": cpu_model(),
         "sample": f"{sample.rows} rows x {sample.cols} cols, blowup {1 << sample.log_blowup}, "
                   f"LDE + Merkle root + fold k={wl.fold_k}; {dt:.2f} s wall",
@@ -298,6 +313,7 @@ def alg_bytes(wl, lens):
     fold reads the codeword and writes one EF element per row."""
     n, w = wl.codeword_rows, wl.cols
     out = {"lde": wl.elems * 8 + n * w * 8, "merkle": sum(lens) * 64}
+    out["lde+merkle"] = out["lde"] + out["merkle"]
     if wl.fold_k:
         out["fold"] = n * w * 8 + n * 16
     return out
@@ -336,7 +352,7 @@ def main():
 
     from zkie_amd import _native as N
     from zkie_amd import configs as C
-    from zkie_amd.pcs import fold_rows_device, lde_device
+    from zkie_amd.pcs import fold_rows_device
     from zkie_amd._native import DeviceBuffer
 
     wl = C.CONFIGS[args.config]
@@ -355,8 +371,14 @@ def main():
     stream = N.Stream()
 
     def step():
-        lde_device(d_in, wl.rows, w, wl.log_blowup, d_cw, stream=stream.handle)
-        N.check(L.zkie_merkle_commit(d_cw.addr, n, w, d_layers.addr, N.p(root), stream.handle), "commit")
+        # encode then commit (zkie_lde_commit: the last NTT pass of 16-wide
+        # rows hashes the rows it produces)
+        if args.no_fuse:
+            N.check(L.zkie_lde_batch(d_in.addr, wl.rows, w, wl.log_blowup, 1, d_cw.addr, stream.handle), "lde")
+            N.check(L.zkie_merkle_commit(d_cw.addr, n, w, d_layers.addr, N.p(root), stream.handle), "commit")
+        else:
+            N.check(L.zkie_lde_commit(d_in.addr, wl.rows, w, wl.log_blowup, 1, d_cw.addr, d_layers.addr,
+                                      N.p(root), stream.handle), "zkie_lde_commit")
         if wl.fold_k:
             fold_rows_device(d_cw, n, wl.fold_k, ch, False, d_fold, stream=stream.handle)
 
@@ -405,8 +427,9 @@ def main():
     dom_roof = roofline(dom_avg_s, dom_bytes, dom_valu, valu_peak, dom_traffic)
 
     stages = {}
+    fused = "ntt_last_leaf" in per_kernel
     for st, names in STAGE_KERNELS.items():
-        if st not in ab:
+        if st not in ab or (fused and st in ("lde", "merkle")) or (not fused and st == "lde+merkle"):
             continue
         ms = sum(step_ms.get(k, 0.0) for k in names)
         if not ms:
@@ -417,7 +440,7 @@ def main():
             tr = sum((per_step(k, "fetch_bytes") or 0) + (per_step(k, "write_bytes") or 0)
                      for k in names if k in per_kernel)
         stages[st] = roofline(ms * 1e-3, ab[st], vi, valu_peak, tr)
-    step_bytes = sum(ab.values())
+    step_bytes = ab["lde+merkle"] + ab.get("fold", 0)
     step_valu = sum(s["valu"]["wave_instr"] for s in stages.values() if s["valu"]) if counters else None
     step_roof = roofline(t, step_bytes, step_valu, valu_peak)
 

@@ -142,6 +142,16 @@ int zkie_merkle_layout(uint64_t h, uint32_t *num_layers, uint64_t *layer_lens);
  * (cap height 0). */
 int zkie_merkle_commit(const uint64_t *d_mat, uint64_t h, uint64_t w, uint64_t *d_layers,
                        uint64_t *root, void *stream);
+/* The encode-then-commit of one WHIR commitment (p3-whir
+ * src/pcs/committer/writer.rs:73-85, dft_batch then commit_matrix; the
+ * initial round through adapter.rs:106-113) in one call: the results of
+ * zkie_lde_batch(d_in, h, w, log_blowup, shift, d_out) followed by
+ * zkie_merkle_commit(d_out, h << log_blowup, w, d_layers, root). For 16-wide
+ * rows and a transform of more than one pass, the last NTT pass hashes the
+ * rows it produces, so the codeword is not read back for the leaves. */
+int zkie_lde_commit(const uint64_t *d_in, uint64_t h, uint64_t w, uint32_t log_blowup,
+                    uint64_t shift, uint64_t *d_out, uint64_t *d_layers, uint64_t *root,
+                    void *stream);
 /* Mmcs::open_batch (p3-merkle-tree mmcs/batch.rs:75-121) for n indices at
  * once: rows_out (host, n*w u64) receives the opened rows, siblings_out
  * (host, n*(num_layers-1)*8 u64) the authentication paths, bottom-up. */

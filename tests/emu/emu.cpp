@@ -10,6 +10,7 @@
 #include <cstring>
 #include <vector>
 
+#include "../../zkie_amd/csrc/last_leaf.hpp"
 #include "../../zkie_amd/csrc/ntt_plan.hpp"
 #include "../../zkie_amd/csrc/poseidon2.hpp"
 
@@ -95,6 +96,46 @@ void run_pass_inv(const PassArgs& a, uint32_t T)
         case 7: run_pass_s<7, INV>(a, knz, T); break;
         case 8: run_pass_s<8, INV>(a, knz, T); break;
         default: run_pass_s<9, INV>(a, knz, T); break;
+    }
+}
+
+// The fused last pass + leaf hash (last_leaf.hpp) of the commitment, phase
+// by phase for every thread of every workgroup, kernel thread count.
+template <int S>
+void run_last_leaf_s(const PassArgs& a, uint64_t* digests, uint64_t digests_len, const P2Consts& C, bool d15)
+{
+    constexpr uint32_t T = 256;
+    using LL = LastLeaf<S>;
+    const uint64_t blocks = pass_blocks(a);
+    std::vector<uint64_t> lds(LL::lds_words());
+    using Keep = uint64_t[LL::template rounds<T>()][kStepU][LL::R];
+    std::vector<Keep> keep(T);
+    for (uint64_t bid = 0; bid < blocks; bid++) {
+        const PassTile t = pass_tile(a, bid);
+        for (uint32_t tid = 0; tid < T; tid++) pass_tables<S, kRoleLast>(a, t, tid, T, lds.data());
+        for (int k = 0; k + 1 < pass_steps<S>(); k++)
+            for (uint32_t tid = 0; tid < T; tid++)
+                pass_step<S, 8, false, kRoleLast, kFuseLogV>(k, a, t, pass_lane(a, t, tid), tid, T, lds.data());
+        for (uint32_t tid = 0; tid < T; tid++) last_leaf_step<S, T>(a, t, pass_lane(a, t, tid), tid, lds.data(), keep[tid]);
+        for (uint32_t tid = 0; tid < T; tid++) last_leaf_rows<S, T>(pass_lane(a, t, tid), tid, lds.data(), keep[tid]);
+        for (uint32_t tid = 0; tid < T; tid++) {
+            if (d15)
+                last_leaf_hash<S, T, true>(a, t, tid, lds.data(), digests, digests_len, C);
+            else
+                last_leaf_hash<S, T, false>(a, t, tid, lds.data(), digests, digests_len, C);
+        }
+    }
+}
+
+void run_last_leaf(const PassArgs& a, uint64_t* digests, uint64_t digests_len, const P2Consts& C, bool d15)
+{
+    switch (a.s) {
+        case 4: run_last_leaf_s<4>(a, digests, digests_len, C, d15); break;
+        case 5: run_last_leaf_s<5>(a, digests, digests_len, C, d15); break;
+        case 6: run_last_leaf_s<6>(a, digests, digests_len, C, d15); break;
+        case 7: run_last_leaf_s<7>(a, digests, digests_len, C, d15); break;
+        case 8: run_last_leaf_s<8>(a, digests, digests_len, C, d15); break;
+        default: run_last_leaf_s<9>(a, digests, digests_len, C, d15); break;
     }
 }
 
@@ -222,6 +263,42 @@ int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uin
     for (uint32_t i = 0; i < p.np; i++) {
         const PassArgs a = pass_args(p, i, B, w, in, h, tmp.data(), out, tab.data(), false);
         run_pass(a, threads, false);
+        B -= a.s;
+    }
+    return 0;
+}
+
+// LDE of 16-wide rows with the last pass fused with the leaf hash: out gets
+// the codeword, digests (n * 8 u64) the leaf digests. Returns 1 when the
+// plan's last pass is not fusable (nothing written), 0 on success.
+int emu_lde_leaf(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t* out,
+                 uint64_t* digests, const uint64_t* rc_init, const uint64_t* rc_final, const uint64_t* rc_internal,
+                 uint64_t diag15, int fast_diag)
+{
+    uint32_t lgh = 0;
+    while ((1ull << lgh) < h) lgh++;
+    const uint32_t L = lgh + log_blowup;
+    const std::vector<uint64_t> tab = build_twiddle_tables();
+    const Plan p = make_plan(L, w);
+    const uint64_t n = 1ull << L;
+    std::vector<uint64_t> tmp(n * w);
+    P2Consts c;
+    for (int k = 0; k < 4; k++)
+        for (int i = 0; i < 16; i++) {
+            c.ext[k][i] = rc_init[16 * k + i];
+            c.ext[4 + k][i] = rc_final[16 * k + i];
+        }
+    for (int k = 0; k < 22; k++) c.internal[k] = rc_internal[k];
+    c.diag15 = diag15;
+    uint32_t B = L;
+    for (uint32_t i = 0; i < p.np; i++) {
+        const PassArgs a = pass_args(p, i, B, w, in, h, tmp.data(), out, tab.data(), false);
+        if (a.last) {
+            if (!last_leaf_fusable(a)) return 1;
+            run_last_leaf(a, digests, n * 8, c, fast_diag != 0);
+        } else {
+            run_pass(a, 512, false);
+        }
         B -= a.s;
     }
     return 0;

@@ -17,7 +17,7 @@ _lib = None
 
 def build() -> str:
     deps = [SRC] + [os.path.join(HERE, "..", "..", "zkie_amd", "csrc", f)
-                    for f in ("gl64.hpp", "poseidon2.hpp", "ntt_pass.hpp", "ntt_plan.hpp")]
+                    for f in ("gl64.hpp", "poseidon2.hpp", "ntt_pass.hpp", "ntt_plan.hpp", "last_leaf.hpp")]
     if os.path.exists(LIB) and all(os.path.getmtime(LIB) >= os.path.getmtime(d) for d in deps):
         return LIB
     cmd = [HIPCC, "--offload-host-only", "-O2", "-fPIC", "-shared", "-std=c++17",
@@ -56,6 +56,9 @@ def load():
         L.emu_dft.restype = ctypes.c_int
         L.emu_lde.argtypes = [_u64p, _u64, _u64, ctypes.c_uint32, _u64p, ctypes.c_uint32]
         L.emu_lde.restype = ctypes.c_int
+        L.emu_lde_leaf.argtypes = [_u64p, _u64, _u64, ctypes.c_uint32, _u64p, _u64p, _u64p, _u64p, _u64p,
+                                   _u64, ctypes.c_int]
+        L.emu_lde_leaf.restype = ctypes.c_int
         _lib = L
     return _lib
 

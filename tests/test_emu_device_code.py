@@ -143,3 +143,21 @@ def test_lde_passes_kernel_threads(emu, oracle, lg, w, lb):
     out = np.zeros(((1 << lg) << lb, w), np.uint64)
     assert emu.emu_lde(ptr(x), 1 << lg, w, lb, ptr(out), 512) == 0
     assert (out == oracle.lde_batch(x, lb)).all()
+
+
+@pytest.mark.parametrize("lg,lb", [(8, 2), (10, 2), (12, 2), (11, 3), (13, 3), (16, 2)])
+def test_lde_last_pass_fused_with_leaf_hash(emu, oracle, lg, lb):
+    """The fused last NTT pass + leaf hash of the commitment (last_leaf.hpp),
+    at the kernel's thread count, for last passes of 5 to 9 bits: the
+    codeword and the leaf digests equal the oracle's LDE and layer 0."""
+    w = 16
+    x = oracle.gen_uniform(9 + lg, (1 << lg) * w).reshape(1 << lg, w)
+    n = (1 << lg) << lb
+    out = np.zeros((n, w), np.uint64)
+    dig = np.zeros((n, 8), np.uint64)
+    a, b, c, d = oracle.p2_constants()
+    assert emu.emu_lde_leaf(ptr(x), 1 << lg, w, lb, ptr(out), ptr(dig), ptr(a), ptr(b), ptr(c), d, 1) == 0
+    cw = oracle.lde_batch(x, lb)
+    assert (out == cw).all()
+    layers, _ = oracle.merkle_commit(cw)
+    assert (dig == layers[0].reshape(n, 8)).all()

@@ -206,3 +206,25 @@ def test_profile_counters(native, oracle):
         assert "p2_leaf" in native.profile_names()
     finally:
         native.profile_enable(False)
+
+
+@pytest.mark.parametrize("h,w,lb,shift", [(1 << 8, 16, 2, 1), (1 << 10, 16, 2, 1), (1 << 12, 16, 2, 1),
+                                          (1 << 11, 16, 3, 1), (1 << 13, 16, 3, 1), (1 << 16, 16, 2, 1),
+                                          (1 << 17, 16, 2, 1), (1 << 14, 16, 3, 7), (1 << 12, 8, 2, 1),
+                                          (1 << 10, 32, 2, 1), (64, 16, 1, 1), (1 << 12, 1, 2, 1)])
+def test_lde_commit(native, oracle, h, w, lb, shift):
+    """zkie_lde_commit: codeword, every digest layer and the root equal the
+    oracle's LDE and commitment; 16-wide shapes of 10 to 19 rows' bits take
+    the fused last pass + leaf hash (last passes of 5 to 9 bits), the others
+    the separate leaf kernel."""
+    _case("lde_commit", h, w, lb, shift)
+    x = oracle.gen_uniform(h * 5 + w + lb, h * w).reshape(h, w)
+    tree = pcs.HipMerkleTreeMmcs().lde_commit_device(DeviceBuffer.from_array(x), h, w, lb, shift=shift)
+    cw = oracle.lde_batch(x, lb, shift)
+    assert (tree.d_mat.download().reshape(cw.shape) == cw).all()
+    layers, root = oracle.merkle_commit(cw)
+    got = tree.layers()
+    assert len(got) == len(layers)
+    for a, b in zip(got, layers):
+        assert (a == b).all()
+    assert (tree.root == root).all()

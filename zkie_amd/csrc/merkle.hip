@@ -16,6 +16,8 @@
 #include <mutex>
 #include <vector>
 
+#include "last_leaf.hpp"
+#include "ntt_plan.hpp"
 #include "poseidon2.hpp"
 #include "poseidon2_x16.hpp"
 #include "row_stage.hpp"
@@ -196,6 +198,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
         hash_row<W, D15>(mat + row * (W > 0 ? (uint64_t)W : w), w, st);
         store_digest(digests + row * 8, st);
     }
+}
+
+// The last pass of a 16-wide LDE fused with the leaf hash (last_leaf.hpp):
+// one workgroup per tile of the pass, 256 threads (four workgroups per CU
+// for tiles of up to 256 rows).
+constexpr uint32_t kFuseThreads = 256;
+
+template <int S, bool D15>
+__global__ __launch_bounds__(kFuseThreads) __attribute__((amdgpu_waves_per_eu(4))) void ntt_last_leaf_kernel(
+    PassArgs a, uint64_t* __restrict__ digests)
+{
+    extern __shared__ uint64_t lds[];
+    constexpr uint32_t T = kFuseThreads;
+    const uint32_t tid = threadIdx.x;
+    __builtin_assume(tid < T);
+    const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
+    const PassTile t = pass_tile(a, bid);
+    const PassLane l = pass_lane(a, t, tid);
+    pass_tables<S, kRoleLast>(a, t, tid, T, lds);
+    __syncthreads();
+    pass_step<S, 8, false, kRoleLast, kFuseLogV>(0, a, t, l, tid, T, lds);
+    __syncthreads();
+    if constexpr (Radix<S>::n == 3) {
+        pass_step<S, 8, false, kRoleLast, kFuseLogV>(1, a, t, l, tid, T, lds);
+        __syncthreads();
+    }
+    uint64_t keep[LastLeaf<S>::template rounds<T>()][kStepU][LastLeaf<S>::R];
+    last_leaf_step<S, T>(a, t, l, tid, lds, keep);
+    __syncthreads();
+    last_leaf_rows<S, T>(l, tid, lds, keep);
+    __syncthreads();
+    last_leaf_hash<S, T, D15>(a, t, tid, lds, digests, 0, c_p2);
 }
 
 // Parents [from, to) of `step` children each; slots [to, pad_to) get the
@@ -417,6 +451,75 @@ int build_upper(uint64_t* d_layers, const std::vector<uint64_t>& lens, bool fast
     return ZKIE_OK;
 }
 
+// Launch the fused last pass + leaf hash for pass arguments `a` (the LDS
+// limit raised per device above the 64 KB default).
+template <int S, bool D15>
+hipError_t launch_last_leaf_s(const PassArgs& a, uint64_t* digests, hipStream_t s)
+{
+    const size_t shmem = (size_t)LastLeaf<S>::lds_words() * 8;
+    static std::mutex mu;
+    static size_t raised[kMaxDevices];
+    if (shmem > 64 * 1024) {
+        const int dev = current_device();
+        if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+        std::lock_guard<std::mutex> g(mu);
+        if (shmem > raised[dev]) {
+            const hipError_t e = hipFuncSetAttribute((const void*)&ntt_last_leaf_kernel<S, D15>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+            if (e != hipSuccess) return e;
+            raised[dev] = shmem;
+        }
+    }
+    const uint64_t blocks = pass_blocks(a);
+    dim3 grid;
+    if (blocks <= 0x7FFFFFFFull) {
+        grid = dim3((unsigned)blocks, 1, 1);
+    } else {
+        if ((blocks % 65536) != 0) return hipErrorInvalidValue;
+        grid = dim3(65536u, (unsigned)(blocks / 65536), 1);
+    }
+    ntt_last_leaf_kernel<S, D15><<<grid, kFuseThreads, shmem, s>>>(a, digests);
+    return hipGetLastError();
+}
+
+template <bool D15>
+hipError_t launch_last_leaf(const PassArgs& a, uint64_t* digests, hipStream_t s)
+{
+    switch (a.s) {
+        case 4: return launch_last_leaf_s<4, D15>(a, digests, s);
+        case 5: return launch_last_leaf_s<5, D15>(a, digests, s);
+        case 6: return launch_last_leaf_s<6, D15>(a, digests, s);
+        case 7: return launch_last_leaf_s<7, D15>(a, digests, s);
+        case 8: return launch_last_leaf_s<8, D15>(a, digests, s);
+        default: return launch_last_leaf_s<9, D15>(a, digests, s);
+    }
+}
+
+// The fused pass applies (last_leaf_fusable) and the digests can take
+// 16-byte stores.
+bool fusable_last_pass(const PassArgs& a, const uint64_t* digests)
+{
+    return last_leaf_fusable(a) && ((uintptr_t)digests & 15) == 0;
+}
+
+struct FuseCtx {
+    uint64_t* digests;
+    bool fast;
+    bool used;
+};
+
+int fuse_hook(const PassArgs& a, hipStream_t s, void* ctx)
+{
+    FuseCtx& c = *static_cast<FuseCtx*>(ctx);
+    if (!fusable_last_pass(a, c.digests)) return ZKIE_PASS_NOT_TAKEN;
+    ProfMark m = prof_begin("ntt_last_leaf", s);
+    const hipError_t e = c.fast ? launch_last_leaf<true>(a, c.digests, s) : launch_last_leaf<false>(a, c.digests, s);
+    prof_end(m, s);
+    ZK_TRY(e);
+    c.used = true;
+    return ZKIE_OK;
+}
+
 }  // namespace
 
 // Exposed to the other translation units of the library.
@@ -431,6 +534,40 @@ int merkle_commit_device(const uint64_t* d_mat, uint64_t h, uint64_t w, uint64_t
     if (rc) return rc;
     if (lens[0] > h) {
         rc = launch_compress(nullptr, d_layers, h, h, lens[0], 2, fast, s);  // zero digests only
+        if (rc) return rc;
+    }
+    if (lens.size() == 1) return ZKIE_OK;
+    return build_upper(d_layers, lens, fast, s);
+}
+
+// The LDE of d_in into d_cw followed by the commitment of its rows into
+// d_layers: the last NTT pass hashes the rows it produces when it can
+// (fusable_last_pass), otherwise the leaf kernel hashes the finished codeword.
+int lde_commit_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+                      uint64_t* d_cw, uint64_t* d_layers, hipStream_t s)
+{
+    if (h == 0 || (h & (h - 1)) != 0 || log_blowup > 32 || !d_layers || (w > 0 && (!d_in || !d_cw)))
+        return ZKIE_ERR_INVALID;
+    uint32_t lgh = 0;
+    while ((1ull << lgh) < h) lgh++;
+    if (lgh + log_blowup > 32) return ZKIE_ERR_INVALID;
+    const uint64_t n = h << log_blowup;
+    bool fast = false;
+    int rc = ensure_constants(&fast);
+    if (rc) return rc;
+    FuseCtx ctx{d_layers, fast, false};
+    const LastPassHook hook{fuse_hook, &ctx};
+    if (w > 0) {
+        rc = lde_run(d_in, h, w, log_blowup, shift, d_cw, s, nullptr, &hook);
+        if (rc) return rc;
+    }
+    const std::vector<uint64_t> lens = layer_lens(n);
+    if (!ctx.used) {
+        rc = launch_leaves(d_cw, d_layers, 0, n, w, fast, s);
+        if (rc) return rc;
+    }
+    if (lens[0] > n) {
+        rc = launch_compress(nullptr, d_layers, n, n, lens[0], 2, fast, s);  // zero digests only
         if (rc) return rc;
     }
     if (lens.size() == 1) return ZKIE_OK;
@@ -531,6 +668,22 @@ int zkie_merkle_commit(const uint64_t* d_mat, uint64_t h, uint64_t w, uint64_t* 
     if (rc) return rc;
     if (root) {
         const std::vector<uint64_t> lens = layer_lens(h);
+        uint64_t off = 0;
+        for (size_t i = 0; i + 1 < lens.size(); i++) off += lens[i] * 8;
+        ZK_TRY(hipMemcpyAsync(root, d_layers + off, 64, hipMemcpyDeviceToHost, s));
+        ZK_TRY(hipStreamSynchronize(s));
+    }
+    return ZKIE_OK;
+}
+
+int zkie_lde_commit(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+                    uint64_t* d_out, uint64_t* d_layers, uint64_t* root, void* stream)
+{
+    hipStream_t s = as_stream(stream);
+    int rc = lde_commit_device(d_in, h, w, log_blowup, shift, d_out, d_layers, s);
+    if (rc) return rc;
+    if (root) {
+        const std::vector<uint64_t> lens = layer_lens(h << log_blowup);
         uint64_t off = 0;
         for (size_t i = 0; i + 1 < lens.size(); i++) off += lens[i] * 8;
         ZK_TRY(hipMemcpyAsync(root, d_layers + off, 64, hipMemcpyDeviceToHost, s));

@@ -73,5 +73,5 @@ extern "C" int zkie_lde_batch_noalloc(const uint64_t* d_in, uint64_t h, uint64_t
     ws.coset = base;
     ws.ntt = base + kCosetWords;
     ws.ntt_words = kNttWords;
-    return lde_run(d_in, h, w, log_blowup, shift, d_out, as_stream(stream), &ws);
+    return lde_run(d_in, h, w, log_blowup, shift, d_out, as_stream(stream), &ws, nullptr);
 }

@@ -231,9 +231,11 @@ __global__ __launch_bounds__(256) void coset_scale_kernel(const uint64_t* __rest
     }
 }
 
-// Run all passes (see pass_args for the buffer roles).
+// Run all passes (see pass_args for the buffer roles). A hook, when given,
+// is offered the last pass of a multi-pass plan first; it returns
+// ZKIE_PASS_NOT_TAKEN to leave that pass to the plain kernel.
 int run_passes(const Plan& p, uint64_t w, const uint64_t* in, uint64_t in_rows, uint64_t* tmp,
-               uint64_t* out, bool inverse, hipStream_t s)
+               uint64_t* out, bool inverse, hipStream_t s, const LastPassHook* hook = nullptr)
 {
     const uint64_t* tables = nullptr;
     int rc = ensure_tables(&tables);
@@ -241,13 +243,17 @@ int run_passes(const Plan& p, uint64_t w, const uint64_t* in, uint64_t in_rows, 
     uint32_t B = p.L;
     for (uint32_t i = 0; i < p.np; i++) {
         const PassArgs a = pass_args(p, i, B, w, in, in_rows, tmp, out, tables, inverse);
+        B -= a.s;
+        if (hook && a.last && p.np > 1) {
+            rc = hook->fn(a, s, hook->ctx);
+            if (rc != ZKIE_PASS_NOT_TAKEN) return rc;
+        }
         const uint64_t blocks = pass_blocks(a);
         ProfMark m = prof_begin(a.last ? "ntt_pass_last" : (i == 0 ? "ntt_pass_first" : "ntt_pass_mid"), s);
         const hipError_t e = inverse ? launch_pass<true>(a, pass_knz(a), blocks, pass_lds_bytes(a), s)
                                      : launch_pass<false>(a, pass_knz(a), blocks, pass_lds_bytes(a), s);
         prof_end(m, s);
         ZK_TRY(e);
-        B -= a.s;
     }
     return ZKIE_OK;
 }
@@ -269,7 +275,7 @@ int dft_inplace(uint64_t* d_mat, uint64_t* d_tmp, uint32_t lg, uint64_t w, bool 
 }  // namespace
 
 int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
-            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws)
+            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws, const LastPassHook* hook)
 {
     if (h == 0 || (h & (h - 1)) != 0 || !d_in || !d_out) return ZKIE_ERR_INVALID;
     uint32_t lgh = 0;
@@ -312,17 +318,17 @@ int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, u
         }
         return run_passes(p, w, src, h, nullptr, d_out, false, s);
     }
-    if (ws) return run_passes(p, w, src, h, ws->ntt, d_out, false, s);
+    if (ws) return run_passes(p, w, src, h, ws->ntt, d_out, false, s, hook);
     Scratch lease(WS_NTT, n * w * 8, s);
     if (lease.status()) return lease.status();
-    return run_passes(p, w, src, h, (uint64_t*)lease.get(), d_out, false, s);
+    return run_passes(p, w, src, h, (uint64_t*)lease.get(), d_out, false, s, hook);
 }
 
 // Exposed to the other translation units of the library.
 int lde_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
                uint64_t* d_out, hipStream_t s)
 {
-    return lde_run(d_in, h, w, log_blowup, shift, d_out, s, nullptr);
+    return lde_run(d_in, h, w, log_blowup, shift, d_out, s, nullptr, nullptr);
 }
 
 // Prefix order (writer.rs:43-71): entry (i, j) of the committed matrix, row

@@ -81,8 +81,20 @@ struct LdeWorkspace {
     uint64_t* coset = nullptr;
 };
 
-// zkie_lde_batch with the work buffers of `ws`, or leased ones when ws is null.
+struct PassArgs;
+
+// A replacement for the last pass of a multi-pass LDE (the fused last pass
+// and leaf hash of the commitment): fn launches it for the pass arguments a
+// on stream s, or returns ZKIE_PASS_NOT_TAKEN to leave it to the plain pass.
+constexpr int ZKIE_PASS_NOT_TAKEN = 1;
+struct LastPassHook {
+    int (*fn)(const PassArgs& a, hipStream_t s, void* ctx);
+    void* ctx;
+};
+
+// zkie_lde_batch with the work buffers of `ws`, or leased ones when ws is
+// null; `hook` (may be null) is offered the last pass.
 int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
-            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws);
+            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws, const LastPassHook* hook);
 
 }  // namespace zk

@@ -115,6 +115,21 @@ class HipMerkleTreeMmcs:
               "zkie_merkle_commit")
         return HipMerkleTree(d_mat, h, w, d_layers, root)
 
+    def lde_commit_device(self, d_in: DeviceBuffer, h: int, w: int, log_blowup: int,
+                          d_codeword: DeviceBuffer | None = None, shift: int = 1,
+                          stream=None) -> HipMerkleTree:
+        """Encode then commit (writer.rs:73-85) in one call: the LDE of the
+        h x w coefficient rows into d_codeword and the tree of its rows."""
+        n = h << log_blowup
+        if d_codeword is None:
+            d_codeword = DeviceBuffer(n * w)
+        lens = N.merkle_layout(n)
+        d_layers = DeviceBuffer(sum(lens) * 8)
+        root = np.zeros(8, np.uint64)
+        check(N.load().zkie_lde_commit(d_in.addr, h, w, log_blowup, shift, d_codeword.addr, d_layers.addr,
+                                        N.p(root), stream), "zkie_lde_commit")
+        return HipMerkleTree(d_codeword, n, w, d_layers, root)
+
     def commit(self, mat) -> tuple[np.ndarray, HipMerkleTree]:
         m = _as_matrix(mat)
         h, w = m.shape

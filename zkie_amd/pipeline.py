@@ -27,7 +27,7 @@ import numpy as np
 from . import _native as N
 from .configs import (SEED_CHALLENGES, SEED_DATA, SEED_OOD, SEED_QUERIES, SEED_WEIGHTS, Workload,
                       XorShift64, challenges, ef_pow2_chain, query_indices)
-from .pcs import (HipMerkleTree, HipMerkleTreeMmcs, eq_table, fold_rows_at, fold_rows_device, lde_device,
+from .pcs import (HipMerkleTree, HipMerkleTreeMmcs, eq_table, fold_rows_at, fold_rows_device,
                   mle_eval, sumcheck_prove)
 from ._native import DeviceBuffer
 
@@ -62,11 +62,8 @@ def commit_round(d_coeffs: DeviceBuffer, h: int, w: int, log_blowup: int,
                  mmcs: HipMerkleTreeMmcs, d_codeword: DeviceBuffer | None = None,
                  stream=None) -> RoundOutput:
     n = h << log_blowup
-    if d_codeword is None:
-        d_codeword = DeviceBuffer(n * w)
-    lde_device(d_coeffs, h, w, log_blowup, d_codeword, stream=stream)
-    tree = mmcs.commit_device(d_codeword, n, w, stream=stream)
-    return RoundOutput(n, w, d_codeword, tree)
+    tree = mmcs.lde_commit_device(d_coeffs, h, w, log_blowup, d_codeword, stream=stream)
+    return RoundOutput(n, w, tree.d_mat, tree)
 
 
 def open_round(rnd: RoundOutput, mmcs: HipMerkleTreeMmcs, count: int, g: XorShift64):
