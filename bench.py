@@ -573,10 +573,13 @@ def ingest_counters(d: str):
         for key, vs in per.items():
             kernels.setdefault(key, {})[field + "_per_step"] = sum(vs) / steps_profiled
             kernels[key]["launches_per_step"] = len(vs) / steps_profiled
-    # Name the NTT passes by their order in the step.
+    # Name the NTT passes by their order in the step, as the library's timers
+    # do (with the last pass fused with the leaf hash, no plain last pass).
     names = {}
+    fused = "ntt_last_leaf" in kernels
     for i, k in enumerate(ntt_order):
-        names[k] = "ntt_pass_first" if i == 0 else ("ntt_pass_last" if i == len(ntt_order) - 1 else "ntt_pass_mid")
+        last = i == len(ntt_order) - 1 and not fused
+        names[k] = "ntt_pass_first" if i == 0 else ("ntt_pass_last" if last else "ntt_pass_mid")
     out = {}
     for k, v in kernels.items():
         out[names.get(k, k)] = dict(v, rocprof_name=k)

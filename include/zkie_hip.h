@@ -225,6 +225,23 @@ int zkie_sumcheck_fold(const uint64_t *d_f, int f_is_ext, const uint64_t *d_h, u
  * (EF, bit 0 of x first, mle.rs:44-56), so that sum_x eq(p, x) f(x) = f(p)
  * (mle.rs:8-22). point (host): num_vars EF coordinates. */
 int zkie_eq_table(const uint64_t *point, uint32_t num_vars, uint64_t *d_out, void *stream);
+/* The batched constraint of a WHIR round (p3-whir src/pcs/prover/mod.rs:228-314):
+ * the out-of-domain claims as evaluation constraints (Statements::Eq) and the
+ * STIR openings as selection constraints (Statements::Select), combined by the
+ * powers of gamma into one weight table over the round table of 2^num_vars
+ * entries, the weights its sumcheck adds to its own:
+ *   d_w[x] (+)= sum_{j<m} gamma^j eq(p_j, x) + sum_{k<q} gamma^(m+k) z_k^x
+ * (EF flattened [c0, c1]; eq as zkie_eq_table, bit b of x variable b; z^x the
+ * powers of a univariate point, so that sum_x f(x) z^x is the value at z of
+ * the polynomial whose coefficients are the table, i.e. the queried-row fold).
+ * eq_points (host): m points of num_vars EF coordinates; sel_points (host): q
+ * EF points; gamma (host): one EF. accumulate = 1 adds to d_w, 0 overwrites
+ * it. The call does not wait for the host or the device. The order of the
+ * powers (the Eq group first, from gamma^0) restates Constraint::new of the
+ * external p3-sumcheck crate. */
+int zkie_constraint_weights(const uint64_t *eq_points, uint32_t m, const uint64_t *sel_points,
+                            uint32_t q, const uint64_t *gamma, uint32_t num_vars, int accumulate,
+                            uint64_t *d_w, void *stream);
 /* zkie_sumcheck_prove: `rounds` rounds with the challenges r (host, rounds EF)
  * given up front, as sumcheck::prove takes them: polys (host) receives
  * 6 u64 per round, d_f_out / d_h_out the tables after the last fold

@@ -73,6 +73,7 @@ def lib():
             "or_mle_eval_base": (u64, [_u64p, u32, _u64p]),
             "or_mle_eval": (None, [_u64p, u32, ctypes.c_int, _u64p, _u64p]),
             "or_eq_table": (None, [_u64p, u32, _u64p]),
+            "or_constraint_weights": (None, [_u64p, u32, _u64p, u32, _u64p, u32, _u64p]),
             "or_sumcheck_prove": (None, [_u64p, ctypes.c_int, _u64p, u32, u32, _u64p, _u64p, _u64p,
                                          _u64p]),
             "or_xorshift_next": (u64, [_u64p]),
@@ -359,6 +360,20 @@ def eq_table(point) -> np.ndarray:
     t = pt.size // 2
     out = np.zeros((1 << t, 2), np.uint64)
     lib().or_eq_table(_p(pt) if pt.size else _p(out), t, _p(out))
+    return out
+
+
+def constraint_weights(eq_points, sel_points, gamma, n: int) -> np.ndarray:
+    """Batched constraint weights of a WHIR round: (2^n, 2) EF,
+    sum_j gamma^j eq(p_j, x) + sum_k gamma^(m+k) z_k^x."""
+    eqp = u64(eq_points).reshape(len(eq_points), n, 2) if len(eq_points) else np.zeros((0, n, 2), np.uint64)
+    sel = u64(sel_points).reshape(-1, 2) if len(sel_points) else np.zeros((0, 2), np.uint64)
+    g = u64(gamma).reshape(2)
+    out = np.zeros((1 << n, 2), np.uint64)
+    dummy = np.zeros(2, np.uint64)
+    lib().or_constraint_weights(_p(np.ascontiguousarray(eqp)) if eqp.size else _p(dummy), eqp.shape[0],
+                                _p(np.ascontiguousarray(sel)) if sel.size else _p(dummy), sel.shape[0],
+                                _p(g), n, _p(out))
     return out
 
 

@@ -630,6 +630,46 @@ void or_eq_table(const uint64_t *point, uint32_t t, uint64_t *out)
     }
 }
 
+/* The batched constraint of a WHIR round (p3-whir src/pcs/prover/mod.rs:228-314):
+ * Constraint::new(gamma, n, [Statements::Eq(ood), Statements::Select(stir)])
+ * as one weight table over the 2^n-entry round table,
+ *   out[x] = sum_{j<m} gamma^j eq(p_j, x) + sum_{k<q} gamma^(m+k) z_k^x,
+ * eq(p, x) as or_eq_table (bit b of x is variable b) and z^x the powers of a
+ * univariate point (the select weight: sum_x f(x) z^x is the value at z of the
+ * polynomial whose coefficients are the table). The p3-sumcheck crate that
+ * defines the combination is external to the reference: the order of the
+ * powers (the Eq group first, from gamma^0) is not pinned by its files. */
+void or_constraint_weights(const uint64_t *eq_points, uint32_t m, const uint64_t *sel, uint32_t q,
+                           const uint64_t gamma[2], uint32_t n, uint64_t *out)
+{
+    const uint64_t N = 1ULL << n;
+    uint64_t *tab = (uint64_t *)malloc(2 * N * sizeof(uint64_t));
+    uint64_t g[2] = {1, 0};
+    const uint64_t gm[2] = {gamma[0] % OR_P, gamma[1] % OR_P};
+    memset(out, 0, 2 * N * sizeof(uint64_t));
+    for (uint32_t c = 0; c < m + q; c++) {
+        if (c < m) {
+            or_eq_table(eq_points + 2 * (uint64_t)c * n, n, tab);
+        } else {
+            const uint64_t z[2] = {sel[2 * (c - m)] % OR_P, sel[2 * (c - m) + 1] % OR_P};
+            tab[0] = 1;
+            tab[1] = 0;
+            for (uint64_t x = 1; x < N; x++) or_ef_mul(tab + 2 * (x - 1), z, tab + 2 * x);
+        }
+#pragma omp parallel for schedule(static)
+        for (int64_t x = 0; x < (int64_t)N; x++) {
+            uint64_t t[2];
+            or_ef_mul(g, tab + 2 * x, t);
+            ef_add(out + 2 * x, t, out + 2 * x);
+        }
+        uint64_t ng[2];
+        or_ef_mul(g, gm, ng);
+        g[0] = ng[0];
+        g[1] = ng[1];
+    }
+    free(tab);
+}
+
 /* common/sumcheck.rs:33-89 (prove and fold) with EF tables and challenges. */
 void or_sumcheck_prove(const uint64_t *f, int f_is_ext, const uint64_t *h, uint32_t t, uint32_t rounds,
                        const uint64_t *r, uint64_t *polys, uint64_t *f_out, uint64_t *h_out)

@@ -129,6 +129,11 @@ void or_sumcheck_prove(const uint64_t *f, int f_is_ext, const uint64_t *h, uint3
 /* eq(p, x) = prod_b (x_b ? p_b : 1 - p_b) for x < 2^t, bit 0 first (mle.rs:44-56),
  * EF point (t coordinates), out: 2^t EF entries. */
 void or_eq_table(const uint64_t *point, uint32_t t, uint64_t *out);
+/* Batched constraint weights of a WHIR round (p3-whir prover/mod.rs:228-314):
+ * out[x] = sum_{j<m} gamma^j eq(p_j, x) + sum_{k<q} gamma^(m+k) z_k^x, x < 2^n
+ * (EF). eq_points: m points of n EF coordinates (variable 0 first); sel: q EF. */
+void or_constraint_weights(const uint64_t *eq_points, uint32_t m, const uint64_t *sel, uint32_t q,
+                           const uint64_t gamma[2], uint32_t n, uint64_t *out);
 
 /* ---- inputs (field.rs:17-36, fixed_point.rs:11-38) ---- */
 uint64_t or_xorshift_next(uint64_t *state);

@@ -13,7 +13,7 @@ import pytest
 
 from zkie_amd import configs as C
 from zkie_amd import pipeline as PL
-from zkie_amd._native import DeviceBuffer, check
+from zkie_amd._native import DeviceBuffer, check, p
 
 pytestmark = pytest.mark.gpu
 
@@ -144,16 +144,20 @@ def test_workload_full_size_properties(native, oracle, number):
 
 @pytest.mark.gpu
 def test_whir_rounds_ood_and_stir_full_size(native, oracle):
-    """The WHIR-shaped workload at full size: every round's out-of-domain
+    """The WHIR-shaped workload at full size: every round's sumcheck weights
+    (the initial evaluation constraint, then the folded weights plus each
+    round's batched OOD + STIR constraint) and round polynomials equal the
+    oracle's, every round's out-of-domain
     answers equal the oracle's multilinear evaluation of the folded table,
     the STIR row folds equal the oracle's fold of the opened rows, and each
     row fold agrees with the next codeword (FRI/STIR consistency): the fold
     of row t of a codeword with N rows is sum_c w_N^(c t) C'[t mod N/2^k][c]."""
     wl = C.CONFIGS[5]
-    print("CASE whir rounds OOD + STIR", wl.name, flush=True)
+    print("CASE whir rounds OOD + STIR + batched constraints", wl.name, flush=True)
     k = wl.fold_k
     out = PL.run_workload(wl, DeviceBuffer.from_array(PL.workload_inputs(wl)), with_openings=False)
     assert len(out.rounds) == wl.rounds + 1
+    weights = None
     for r in range(1, len(out.rounds)):
         prev, rnd = out.rounds[r - 1], out.rounds[r]
         table, t_entries = out.tables[r - 1]
@@ -161,13 +165,20 @@ def test_whir_rounds_ood_and_stir_full_size(native, oracle):
         n_vars = t_entries.bit_length() - 1
         for z, ans in zip(rnd.ood_points, rnd.ood_answers):
             assert (ans == oracle.mle_eval(tab, C.ef_pow2_chain(z, n_vars), True)).all()
-        # the sumcheck rounds that folded the previous table (its weight: the
-        # eq table of the round's evaluation constraint)
+        # the sumcheck rounds that folded the previous table, with the running
+        # weights: the initial evaluation constraint, then after every round
+        # the folded weights plus that round's batched constraint
         ch = C.challenges(k * wl.rounds)[k * (r - 1):k * r]
         prev_tab = (PL.workload_inputs(wl).reshape(-1) if r == 1 else out.tables[r - 2][0].download())
-        polys, f_out, _ = oracle.sumcheck_prove(prev_tab, r > 1, oracle.eq_table(rnd.weight_point), ch)
+        if r == 1:
+            weights = oracle.eq_table(rnd.weight_point)
+        polys, f_out, h_out = oracle.sumcheck_prove(prev_tab, r > 1, weights, ch)
         assert (rnd.sumcheck_polys == polys).all()
         assert (tab.reshape(-1, 2) == f_out).all()
+        eq_pts = np.array([C.ef_pow2_chain(z, n_vars) for z in rnd.ood_points], np.uint64)
+        w_c = oracle.constraint_weights(eq_pts, rnd.stir_points, rnd.gamma, n_vars)
+        weights = ((h_out.astype(object) + w_c.astype(object)) % C.P).astype(np.uint64)
+        assert (rnd.weights.download().reshape(-1, 2) == weights).all()
         idx = rnd.stir_indices.astype(np.int64)
         prev_cw = prev.codeword.download().reshape(prev.rows, prev.width)
         ch = C.challenges(k * wl.rounds)[k * (r - 1):k * r]
@@ -183,3 +194,57 @@ def test_whir_rounds_ood_and_stir_full_size(native, oracle):
                 acc0 = (acc0 + wc * int(cw[t % M, c, 0])) % C.P
                 acc1 = (acc1 + wc * int(cw[t % M, c, 1])) % C.P
             assert [acc0, acc1] == [int(f[0]), int(f[1])]
+
+
+def _ef_mul(a, b):
+    return ((a[0] * b[0] + 7 * a[1] * b[1]) % C.P, (a[0] * b[1] + a[1] * b[0]) % C.P)
+
+
+def _poly_at(poly, x):
+    """c0 + c1 x + c2 x^2 in EF."""
+    c = [(int(poly[i][0]), int(poly[i][1])) for i in range(3)]
+    x = (int(x[0]), int(x[1]))
+    acc = c[2]
+    for i in (1, 0):
+        acc = _ef_mul(acc, x)
+        acc = ((acc[0] + c[i][0]) % C.P, (acc[1] + c[i][1]) % C.P)
+    return acc
+
+
+def test_whir_batched_constraints_full_size(native, oracle):
+    """The WHIR-shaped workload at full size, checked the way its verifier
+    combines the claims (p3-whir verifier/mod.rs:158-180): the sum over the
+    round table of table x batched weights equals the batched claim
+    sum_j gamma^j ood_j + sum_k gamma^(m+k) stir_k (the STIR claims are the
+    queried-row folds, the values of the table's polynomial at w_N^index), and
+    each round's first sumcheck polynomial sums over {0, 1} to the previous
+    sumcheck's final claim plus that batched claim."""
+    from zkie_amd import pcs
+
+    wl = C.CONFIGS[5]
+    print("CASE whir batched constraints", wl.name, flush=True)
+    k = wl.fold_k
+    out = PL.run_workload(wl, DeviceBuffer.from_array(PL.workload_inputs(wl)), with_openings=False)
+    ch = C.challenges(k * wl.rounds)
+    for r in range(1, len(out.rounds)):
+        rnd = out.rounds[r]
+        table, t_entries = out.tables[r - 1]
+        n_vars = t_entries.bit_length() - 1
+        eq_pts = np.array([C.ef_pow2_chain(z, n_vars) for z in rnd.ood_points], np.uint64)
+        w = pcs.constraint_weights(eq_pts, rnd.stir_points, rnd.gamma, n_vars)
+        y = np.zeros(6, np.uint64)
+        check(native.load().zkie_sumcheck_round(table.addr, 1, w.addr, n_vars, p(y), None), "round")
+        c0, c1, c2 = (int(y[0]), int(y[1])), (int(y[2]), int(y[3])), (int(y[4]), int(y[5]))
+        # p(0) + p(1) = 2 c0 + c1 + c2
+        total = ((2 * c0[0] + c1[0] + c2[0]) % C.P, (2 * c0[1] + c1[1] + c2[1]) % C.P)
+        assert total == (int(rnd.claim[0]), int(rnd.claim[1])), r
+        if r + 1 < len(out.rounds):
+            # next round's sumcheck: its first polynomial sums to the claim
+            # left by this round's sumcheck plus this round's batched claim
+            last = _poly_at(rnd.sumcheck_polys[-1], ch[k * (r - 1) + k - 1])
+            nxt = out.rounds[r + 1].sumcheck_polys[0]
+            s0 = _poly_at(nxt, (0, 0))
+            s1 = _poly_at(nxt, (1, 0))
+            got = ((s0[0] + s1[0]) % C.P, (s0[1] + s1[1]) % C.P)
+            want = ((last[0] + int(rnd.claim[0])) % C.P, (last[1] + int(rnd.claim[1])) % C.P)
+            assert got == want, r

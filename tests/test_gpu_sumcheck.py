@@ -107,3 +107,46 @@ def test_eq_table_matches_oracle(native, oracle, t):
     print(f"CASE eq_table t={t}", flush=True)
     pt = (oracle.gen_uniform(1500 + t, 2 * t) % np.uint64(P)).reshape(t, 2)
     assert (pcs.eq_table(pt).download().reshape(-1, 2) == oracle.eq_table(pt)).all()
+
+
+@pytest.mark.parametrize("n,m,q,acc", [(0, 1, 0, False), (3, 1, 2, False), (7, 0, 3, True), (8, 2, 5, True),
+                                       (9, 2, 0, False), (12, 2, 100, False), (16, 5, 30, True),
+                                       (18, 2, 128, True), (11, 0, 0, False), (11, 0, 0, True)])
+def test_constraint_weights_match_oracle(native, oracle, n, m, q, acc):
+    """zkie_constraint_weights (the batched constraint of a WHIR round) equals
+    the oracle bit for bit: tables split at 8 or more low bits, several
+    launches when the points exceed one launch's arguments (m n + q > 96),
+    added to or overwriting the running weights."""
+    from zkie_amd import pcs
+    from zkie_amd._native import DeviceBuffer
+
+    print(f"CASE constraint_weights n={n} m={m} q={q} acc={acc}", flush=True)
+    pts = (oracle.gen_uniform(3000 + n, 2 * m * n) % np.uint64(P)).reshape(m, n, 2)
+    sel = (oracle.gen_uniform(3100 + n, 2 * q) % np.uint64(P)).reshape(q, 2)
+    gamma = oracle.gen_uniform(3200 + n, 2) % np.uint64(P)
+    base = oracle.gen_uniform(3300 + n, 2 << n) % np.uint64(P)
+    d_w = DeviceBuffer.from_array(base)
+    pcs.constraint_weights(pts, sel, gamma, n, d_w=d_w, accumulate=acc)
+    exp = oracle.constraint_weights(pts if m else [], sel if q else [], gamma, n)
+    if acc:
+        exp = ((exp.astype(object) + base.reshape(-1, 2).astype(object)) % P).astype(np.uint64)
+    assert (d_w.download().reshape(-1, 2) == exp).all()
+
+
+def test_constraint_weights_on_a_stream(native, oracle):
+    """Queued on a non-null stream after a kernel that writes the running
+    weights, with nothing waiting for the host in between."""
+    from zkie_amd import pcs
+    from zkie_amd._native import DeviceBuffer, Stream
+
+    print("CASE constraint_weights stream", flush=True)
+    s = Stream()
+    n = 14
+    pt = (oracle.gen_uniform(3400, 2 * n) % np.uint64(P)).reshape(n, 2)
+    sel = (oracle.gen_uniform(3401, 40) % np.uint64(P)).reshape(20, 2)
+    gamma = np.array([3, 4], np.uint64)
+    d_w = pcs.eq_table(pt, s.handle)
+    pcs.constraint_weights([], sel, gamma, n, d_w=d_w, accumulate=True, stream=s.handle)
+    s.synchronize()
+    exp = (oracle.eq_table(pt).astype(object) + oracle.constraint_weights([], sel, gamma, n).astype(object)) % P
+    assert (d_w.download().reshape(-1, 2) == exp.astype(np.uint64)).all()

@@ -54,6 +54,7 @@ SIGNATURES = {
     "zkie_whir_encode": [_vp, _u32, _int, _u32, _u32, _int, _vp, _vp],
     "zkie_sumcheck_round": [_vp, _int, _vp, _u32, _u64p, _vp],
     "zkie_eq_table": [_u64p, _u32, _vp, _vp],
+    "zkie_constraint_weights": [_u64p, _u32, _u64p, _u32, _u64p, _u32, _int, _vp, _vp],
     "zkie_sumcheck_fold": [_vp, _int, _vp, _u32, _u64p, _vp, _vp, _u64p, _vp],
     "zkie_sumcheck_prove": [_vp, _int, _vp, _u32, _u32, _u64p, _u64p, _vp, _vp, _vp],
     "zkie_prover_data_size": [_u64, _u64, _u64p],

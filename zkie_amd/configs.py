@@ -1,6 +1,7 @@
 """The synthetic commitment workloads (shapes, generators, seeds).
 
-Seeds: data 0, fold challenges 1, query indices 2, out-of-domain points 3. Inputs come from the
+Seeds: data 0, fold challenges 1, query indices 2, out-of-domain points 3,
+the initial evaluation constraint 4, the constraint-batching challenges 5. Inputs come from the
 XorShift64 generator of common/field.rs:17-36 (zkie_gen_inputs).
   1  2^16 int16 values, one column, blowup 4 -> 2^18-row codeword, Merkle root.
   2  GPT-2-small 768x3072 weight matrix, Irwin-Hall gaussian int16
@@ -23,7 +24,7 @@ from dataclasses import dataclass
 import numpy as np
 
 GEN_UNIFORM, GEN_I16, GEN_I8, GEN_GAUSS_I16 = 0, 1, 2, 3
-SEED_DATA, SEED_CHALLENGES, SEED_QUERIES, SEED_OOD, SEED_WEIGHTS = 0, 1, 2, 3, 4
+SEED_DATA, SEED_CHALLENGES, SEED_QUERIES, SEED_OOD, SEED_WEIGHTS, SEED_GAMMA = 0, 1, 2, 3, 4, 5
 P = 0xFFFFFFFF00000001
 
 

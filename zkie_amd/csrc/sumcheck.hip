@@ -12,6 +12,7 @@
 // [c0, c1]; challenges are EF. Both kernels stream their tables once
 // (HBM-bound): the round kernel reduces its three EF sums per workgroup in
 // LDS and one small workgroup adds the partial sums.
+#include <algorithm>
 #include <vector>
 
 #include "gl64.hpp"
@@ -282,40 +283,174 @@ int sc_fold(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, co
 
 // eq(p, x) = prod_b (x_b ? p_b : 1 - p_b) for x < 2^n (bit 0 first):
 // lo[x mod 2^L] * hi[x >> L], both halves formed on the host.
-__global__ __launch_bounds__(kScThreads) void sc_eq_kernel(const uint64_t* __restrict__ lo,
-                                                           const uint64_t* __restrict__ hi, uint32_t L,
-                                                           uint64_t n, uint64_t* __restrict__ out)
-{
-    const uint64_t x = (uint64_t)blockIdx.x * kScThreads + threadIdx.x;
-    if (x >= n) return;
-    const uint64_t a = x & ((1ull << L) - 1), b = x >> L;
-    const Ef e = ef_mul(Ef{lo[2 * a], lo[2 * a + 1]}, Ef{hi[2 * b], hi[2 * b + 1]});
-    out[2 * x] = gl_canon(e.c0);
-    out[2 * x + 1] = gl_canon(e.c1);
-}
+// [a, a + n) and [b, b + m) (u64 counts) share memory.
+bool overlaps(const uint64_t* a, uint64_t n, const uint64_t* b, uint64_t m) { return a < b + m && b < a + n; }
 
-// eq table of the coordinates p[0..k) (EF) into out (2^k EF, host).
-void eq_half_table(const uint64_t* p, uint32_t k, uint64_t* out)
+// ---- batched constraint weights of a WHIR round -----------------------------
+// w[x] (+)= sum_c g_c T_c(x) over constraints c: an evaluation constraint at a
+// point p has T(x) = eq(p, x) = prod_b (x_b ? p_b : 1 - p_b), a selection
+// constraint at a univariate point z has T(x) = z^x = prod_b (x_b ? z^(2^b) :
+// 1), and g_c = gamma^c. Both are products of one factor per bit of x, so
+// with x = x_lo + 2^h x_hi each table splits into lo_c[x_lo] hi_c[x_hi]: one
+// kernel forms those small tables, a second sums lo_c[x_lo] hi_c[x_hi] over
+// c for every x as exact dot products (DotAcc), with hi_c (gamma folded in)
+// read as wave-uniform scalars. The inputs travel as kernel arguments, so
+// the call queues its work without waiting for the host.
+constexpr uint32_t kCwMaxValues = 96;  // EF values per launch: eq coordinates + selection points
+
+struct CwArgs {
+    uint64_t g0[2];     // gamma^(index of the launch's first constraint)
+    uint64_t gamma[2];
+    uint32_t n, h, m, q;  // variables, low bits of the split, eq points, selection points
+    uint64_t v[2 * kCwMaxValues];  // m points of n EF coordinates (variable 0 first), then q EF points
+};
+
+// lo[c][t] (t < 2^h) and hi[c][u] (u < 2^(n-h), stored [c0, c1, 7 c1], times g_c).
+__global__ __launch_bounds__(kScThreads) void cw_tables_kernel(const CwArgs a, uint64_t* __restrict__ lo,
+                                                              uint64_t* __restrict__ hi)
 {
-    out[0] = 1;
-    out[1] = 0;
-    for (uint32_t b = 0; b < k; b++) {
-        const uint64_t m = 1ull << b;
-        const Ef z{gl_canon(p[2 * b]), gl_canon(p[2 * b + 1])};
-        const Ef one_minus{gl_sub(1, z.c0), gl_neg(z.c1)};
-        for (uint64_t j = 0; j < m; j++) {
-            const Ef v{out[2 * j], out[2 * j + 1]};
-            const Ef v1 = ef_mul(v, z), v0 = ef_mul(v, one_minus);
-            out[2 * (j + m)] = gl_canon(v1.c0);
-            out[2 * (j + m) + 1] = gl_canon(v1.c1);
-            out[2 * j] = gl_canon(v0.c0);
-            out[2 * j + 1] = gl_canon(v0.c1);
+    const uint32_t C = a.m + a.q;
+    const uint64_t nlo = (uint64_t)C << a.h, nhi = (uint64_t)C << (a.n - a.h);
+    const uint64_t t = (uint64_t)blockIdx.x * kScThreads + threadIdx.x;
+    if (t >= nlo + nhi) return;
+    const bool is_lo = t < nlo;
+    const uint64_t e = is_lo ? t : t - nlo;
+    const uint32_t bits = is_lo ? a.h : a.n - a.h, b0 = is_lo ? 0 : a.h;
+    const uint32_t c = (uint32_t)(e >> bits);
+    const uint64_t x = e & ((1ull << bits) - 1);
+    Ef acc{1, 0};
+    if (c < a.m) {
+        const uint64_t* p = a.v + 2 * ((uint64_t)c * a.n + b0);
+        for (uint32_t b = 0; b < bits; b++) {
+            const Ef pb{p[2 * b], p[2 * b + 1]};
+            acc = ef_mul(acc, ((x >> b) & 1) ? pb : ef_sub(Ef{1, 0}, pb));
         }
+    } else {
+        const uint64_t* zp = a.v + 2 * ((uint64_t)a.m * a.n + (c - a.m));
+        Ef z{zp[0], zp[1]};
+        for (uint32_t b = 0; b < b0; b++) z = ef_mul(z, z);  // z^(2^h) for the high bits
+        for (uint32_t b = 0; b < bits; b++) {
+            if ((x >> b) & 1) acc = ef_mul(acc, z);
+            z = ef_mul(z, z);
+        }
+    }
+    if (is_lo) {
+        lo[2 * e] = gl_canon(acc.c0);
+        lo[2 * e + 1] = gl_canon(acc.c1);
+    } else {
+        Ef g{a.g0[0], a.g0[1]};
+        const Ef gm{a.gamma[0], a.gamma[1]};
+        for (uint32_t i = 0; i < c; i++) g = ef_mul(g, gm);
+        acc = ef_mul(acc, g);
+        const uint64_t c0 = gl_canon(acc.c0), c1 = gl_canon(acc.c1);
+        hi[3 * e] = c0;
+        hi[3 * e + 1] = c1;
+        hi[3 * e + 2] = gl_canon(gl_mul7(c1));
     }
 }
 
-// [a, a + n) and [b, b + m) (u64 counts) share memory.
-bool overlaps(const uint64_t* a, uint64_t n, const uint64_t* b, uint64_t m) { return a < b + m && b < a + n; }
+// w[x] (+)= sum_{c < C} lo_c[x_lo] hi_c[x_hi] for x < 2^n. Every x of a
+// 256-entry block shares x_hi (2^h >= 256, or h = n), so hi is read at a
+// wave-uniform address.
+__global__ __launch_bounds__(kScThreads) void cw_apply_kernel(const uint64_t* __restrict__ lo,
+                                                             const uint64_t* __restrict__ hi, uint32_t C,
+                                                             uint32_t n, uint32_t h, int accumulate,
+                                                             uint64_t* __restrict__ w)
+{
+    const uint64_t N = 1ull << n, nhi = 1ull << (n - h), lmask = (1ull << h) - 1;
+    for (uint64_t base = (uint64_t)blockIdx.x * kScThreads; base < N; base += (uint64_t)gridDim.x * kScThreads) {
+        const uint64_t x = base + threadIdx.x;
+        if (x >= N) continue;
+        const uint64_t xh = base >> h, xl = x & lmask;
+        DotAcc s0, s1;
+#pragma unroll 2
+        for (uint32_t c = 0; c < C; c++) {
+            const uint64_t* H = hi + 3 * ((uint64_t)c * nhi + xh);
+            const uint64_t h0 = H[0], h1 = H[1], h7 = H[2];
+            const uint64_t* Lp = lo + 2 * (((uint64_t)c << h) + xl);
+            const uint64_t l0 = Lp[0], l1 = Lp[1];
+            // (h0 + h1 X)(l0 + l1 X) = (h0 l0 + 7 h1 l1) + (h0 l1 + h1 l0) X
+            dot_add(s0, h0, l0);
+            dot_add(s0, h7, l1);
+            dot_add(s1, h0, l1);
+            dot_add(s1, h1, l0);
+        }
+        uint64_t c0 = gl_canon(dot_reduce(s0)), c1 = gl_canon(dot_reduce(s1));
+        if (accumulate) {
+            c0 = gl_canon(gl_add(w[2 * x], c0));
+            c1 = gl_canon(gl_add(w[2 * x + 1], c1));
+        }
+        w[2 * x] = c0;
+        w[2 * x + 1] = c1;
+    }
+}
+
+// Launch the weights of m eq points and q selection points (gamma^0 for the
+// first eq point); the inputs are host arrays, copied into kernel arguments.
+int constraint_weights(const uint64_t* eq_points, uint32_t m, const uint64_t* sel, uint32_t q, const uint64_t* gamma,
+                       uint32_t n, int accumulate, uint64_t* d_w, hipStream_t s)
+{
+    const uint32_t h = n <= 8 ? n : (((n + 1) / 2) > 8 ? (n + 1) / 2 : 8);
+    const uint64_t N = 1ull << n;
+    const unsigned apply_grid = (unsigned)std::min<uint64_t>((N + kScThreads - 1) / kScThreads, 65536);
+    const uint32_t total = m + q;
+    if (total == 0) {
+        if (!accumulate) {
+            cw_apply_kernel<<<apply_grid, kScThreads, 0, s>>>(nullptr, nullptr, 0, n, h, 0, d_w);
+            ZK_LAUNCHED();
+        }
+        return ZKIE_OK;
+    }
+    // most constraints one launch can hold (selection points take one value each)
+    const uint64_t per = ((1ull << h) * 2 + (1ull << (n - h)) * 3) * 8;
+    Scratch ws(WS_MISC, (size_t)kCwMaxValues * per, s);
+    if (ws.status()) return ws.status();
+    uint64_t* d_lo = (uint64_t*)ws.get();
+    const Ef gm{gl_canon(gamma[0]), gl_canon(gamma[1])};
+    Ef g{1, 0};
+    uint32_t c = 0;
+    bool first = true;
+    while (c < total) {
+        CwArgs a{};
+        a.gamma[0] = gm.c0;
+        a.gamma[1] = gm.c1;
+        a.g0[0] = gl_canon(g.c0);
+        a.g0[1] = gl_canon(g.c1);
+        a.n = n;
+        a.h = h;
+        // eq points first, then selection points, as many as fit
+        uint32_t used = 0;
+        while (c < m && used + n <= kCwMaxValues) {
+            for (uint32_t b = 0; b < n; b++) {
+                a.v[2 * (used + b)] = gl_canon(eq_points[2 * ((uint64_t)c * n + b)]);
+                a.v[2 * (used + b) + 1] = gl_canon(eq_points[2 * ((uint64_t)c * n + b) + 1]);
+            }
+            used += n;
+            a.m++;
+            c++;
+        }
+        if (c >= m) {
+            while (c < total && used < kCwMaxValues) {
+                a.v[2 * used] = gl_canon(sel[2 * (c - m)]);
+                a.v[2 * used + 1] = gl_canon(sel[2 * (c - m) + 1]);
+                used++;
+                a.q++;
+                c++;
+            }
+        }
+        const uint32_t C = a.m + a.q;
+        uint64_t* d_hi = d_lo + ((uint64_t)C << h) * 2;
+        const uint64_t entries = ((uint64_t)C << h) + ((uint64_t)C << (n - h));
+        ProfMark pm = prof_begin("constraint_weights", s);
+        cw_tables_kernel<<<(unsigned)((entries + kScThreads - 1) / kScThreads), kScThreads, 0, s>>>(a, d_lo, d_hi);
+        cw_apply_kernel<<<apply_grid, kScThreads, 0, s>>>(d_lo, d_hi, C, n, h, first ? accumulate : 1, d_w);
+        prof_end(pm, s);
+        ZK_LAUNCHED();
+        for (uint32_t i = 0; i < C; i++) g = ef_mul(g, gm);
+        first = false;
+    }
+    return ZKIE_OK;
+}
 
 }  // namespace
 }  // namespace zk
@@ -376,21 +511,16 @@ int zkie_sumcheck_fold(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, u
 int zkie_eq_table(const uint64_t* point, uint32_t num_vars, uint64_t* d_out, void* stream)
 {
     if (num_vars > 34 || !d_out || (num_vars && !point)) return ZKIE_ERR_INVALID;
-    hipStream_t s = as_stream(stream);
-    const uint32_t L = (num_vars + 1) / 2, Hb = num_vars - L;
-    std::vector<uint64_t> tabs(2 * ((1ull << L) + (1ull << Hb)));
-    eq_half_table(point, L, tabs.data());
-    eq_half_table(point + 2 * L, Hb, tabs.data() + 2 * (1ull << L));
-    Scratch ws(WS_MISC, tabs.size() * 8, s);
-    if (ws.status()) return ws.status();
-    uint64_t* d_tabs = (uint64_t*)ws.get();
-    ZK_TRY(hipMemcpyAsync(d_tabs, tabs.data(), tabs.size() * 8, hipMemcpyHostToDevice, s));
-    const uint64_t n = 1ull << num_vars;
-    sc_eq_kernel<<<(unsigned)((n + kScThreads - 1) / kScThreads), kScThreads, 0, s>>>(
-        d_tabs, d_tabs + 2 * (1ull << L), L, n, d_out);
-    ZK_LAUNCHED();
-    ZK_TRY(hipStreamSynchronize(s));  // the halves were copied from a host vector
-    return ZKIE_OK;
+    // one evaluation constraint with weight gamma^0 = 1 (no host wait)
+    const uint64_t one[2] = {1, 0};
+    return constraint_weights(point, 1, nullptr, 0, one, num_vars, 0, d_out, as_stream(stream));
+}
+
+int zkie_constraint_weights(const uint64_t* eq_points, uint32_t m, const uint64_t* sel_points, uint32_t q,
+                            const uint64_t* gamma, uint32_t num_vars, int accumulate, uint64_t* d_w, void* stream)
+{
+    if (num_vars > 34 || !d_w || !gamma || (m && !eq_points) || (q && !sel_points)) return ZKIE_ERR_INVALID;
+    return constraint_weights(eq_points, m, sel_points, q, gamma, num_vars, accumulate != 0, d_w, as_stream(stream));
 }
 
 int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, uint32_t num_vars,

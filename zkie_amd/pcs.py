@@ -248,6 +248,26 @@ def eq_table(point, stream=None) -> DeviceBuffer:
     return out
 
 
+def constraint_weights(eq_points, sel_points, gamma, num_vars: int, d_w: DeviceBuffer | None = None,
+                       accumulate: bool = False, stream=None) -> DeviceBuffer:
+    """The batched constraint of a WHIR round (p3-whir prover/mod.rs:228-314) as
+    weights over the round table: d_w[x] (+)= sum_j gamma^j eq(p_j, x) +
+    sum_k gamma^(m+k) z_k^x. eq_points: (m, num_vars, 2) EF; sel_points: (q, 2)."""
+    m = len(eq_points)
+    eqp = np.ascontiguousarray(np.asarray(eq_points, np.uint64).reshape(-1))
+    sel = np.ascontiguousarray(np.asarray(sel_points, np.uint64).reshape(-1))
+    g = np.ascontiguousarray(np.asarray(gamma, np.uint64).reshape(2))
+    assert eqp.size == 2 * m * num_vars, "eq_points: (m, num_vars, 2) EF coordinates"
+    q = sel.size // 2
+    if d_w is None:
+        d_w = DeviceBuffer(2 << num_vars)
+    dummy = np.zeros(2, np.uint64)
+    check(N.load().zkie_constraint_weights(N.p(eqp) if eqp.size else N.p(dummy), m,
+                                           N.p(sel) if sel.size else N.p(dummy), q, N.p(g), num_vars,
+                                           1 if accumulate else 0, d_w.addr, stream), "zkie_constraint_weights")
+    return d_w
+
+
 def sumcheck_fold(d_f: DeviceBuffer, f_is_ext: bool, d_h: DeviceBuffer, num_vars: int, r,
                   stream=None, next_poly: bool = False):
     """Both tables bound at variable 0 to the EF challenge r
