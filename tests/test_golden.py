@@ -103,3 +103,20 @@ def test_gpu_full_size_workload_matches_fixture(native, oracle, number):
         assert f"{oracle.checksum(out.fold.download()):016x}" == ref["fold_checksum"]
     for (buf, _), cs in zip(out.tables, ref.get("table_checksums", [])):
         assert f"{oracle.checksum(buf.download()):016x}" == cs
+
+
+def test_reference_comparison_script_matches_the_oracle(oracle):
+    """tests/golden/compare_reference_answers.py (the check a holder of the
+    external crates runs) states the same constants as the oracle."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("cra", os.path.join(HERE, "golden", "compare_reference_answers.py"))
+    cra = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(cra)
+    w = cra.restated()
+    a, b, c, d = oracle.p2_constants()
+    assert w["p2_constants"]["rc_init"] == [f"{int(x):016x}" for x in a]
+    assert int(w["matrix_diag_16"][15], 16) == d
+    assert [int(x, 16) for x in w["two_adic_generators"]] == [oracle.two_adic_generator(k) for k in range(33)]
+    iota = np.arange(16, dtype=np.uint64)
+    assert [int(x, 16) for x in w["p2_permute_iota"]] == [int(x) for x in oracle.p2_permute(iota)]
