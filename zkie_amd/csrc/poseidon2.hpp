@@ -17,13 +17,14 @@
 //  * corrections that a lane needs only with probability about 2^-32 (the
 //    multiply's final borrow, second wraps, the linear-layer folds) run
 //    behind wave-uniform branches (gl64.hpp);
-//  * the internal diagonal is applied without multiplies: 2^-k splits x
-//    into x >> k and the shifted-out bits, the 2^-32 entry uses a closed form
-//    when diag15 has that value, and 2x, 3x, 4x, -3x are exact sums of
-//    halves or shifts with the wrapped bits folded back once;
-//  * in the internal rounds the work that does not depend on the S-box is
-//    issued before it, and the round sum is made canonical so the sixteen
-//    "sum + t" additions need one wrap correction each;
+//  * the external layer is M4 (x_g + S) per group of four words, S the sum of
+//    the four groups (mds_light16 = circ(2 M4, M4, M4, M4));
+//  * the internal diagonal is applied without multiplies: every output of an
+//    internal round is an exact sum of 32-bit halves built on the unreduced
+//    round sum (2^-k splits x into x >> k and the shifted-out bits, -v x uses
+//    the complement ~x), and the constant that the next step adds to a word
+//    (the next round's rc0, or the terminal round's constants after the last
+//    internal round) joins those sums instead of a separate modular add;
 //  * round loops stay rolled (one copy of the external round body) to keep
 //    the code inside the instruction cache.
 #pragma once
@@ -98,38 +99,44 @@ __host__ __device__ __forceinline__ void mat4_wide(const uint64_t* x, uint64_t* 
     y[2] = t01233 + t23;          // x0 + x1 + 2x2 + 3x3
 }
 
-// st <- mds_light16(st) (+ rc if given). Output 4g + k is mat4(x_g)[k] +
-// sum_h mat4(x_h)[k], and the column sum equals mat4(sum_h x_h)[k] (mat4
-// is linear), so the sums come from the four-lane group sums first and each
-// group is then transformed and written on its own: only one group's
-// intermediate sums are live at a time. Both 32-bit halves of the state go
-// through the layer as exact 64-bit sums (at most 35 (2^32 - 1) + 2^32
-// each), and each output is reduced once from its two sums.
-template <bool ADD_RC>
-__host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_t* rc)
+// st <- mds_light16(st) (+ constants). mds_light16 is circ(2 M4, M4, M4, M4):
+// output group g is M4 x_g + sum_h M4 x_h = M4 (x_g + S) with S the sum of
+// the four groups (M4 is linear), so the column sums S come first and each
+// group is then z = x_g + S and M4 z, written on its own (only one group's
+// intermediate sums are live at a time). Both 32-bit halves of the state go
+// through the layer as exact 64-bit sums (z below 5 2^32, M4 z below 35 2^32
+// plus a constant's half), and each output is reduced once from its two
+// sums. RC: kRcNone, kRcAll (rc[i] added to word i), kRcLane0 (rc[0] added
+// to word 0 only, the constant of the first internal round).
+enum { kRcNone = 0, kRcAll = 1, kRcLane0 = 2 };
+
+template <int RC>
+__host__ __device__ __forceinline__ void mds_light16_rc(uint64_t* st, const uint64_t* rc)
 {
-    uint64_t gl[4], gh[4], sl[4], sh[4];
+    uint64_t sl[4], sh[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        gl[k] = acc32(acc32(acc32m<1>((uint32_t)st[k], (uint32_t)st[4 + k]), (uint32_t)st[8 + k]),
+        sl[k] = acc32(acc32(acc32m<1>((uint32_t)st[k], (uint32_t)st[4 + k]), (uint32_t)st[8 + k]),
                       (uint32_t)st[12 + k]);
-        gh[k] = acc32(acc32(acc32m<1>((uint32_t)(st[k] >> 32), (uint32_t)(st[4 + k] >> 32)),
+        sh[k] = acc32(acc32(acc32m<1>((uint32_t)(st[k] >> 32), (uint32_t)(st[4 + k] >> 32)),
                             (uint32_t)(st[8 + k] >> 32)),
                       (uint32_t)(st[12 + k] >> 32));
     }
-    mat4_wide(gl, sl);
-    mat4_wide(gh, sh);
     uint64_t w[16];  // lanes whose output still needs + eps (one shared rare branch)
 #pragma unroll
     for (int j = 0; j < 16; j += 4) {
-        uint64_t yl[4], yh[4];
-        mat4_half((uint32_t)st[j], (uint32_t)st[j + 1], (uint32_t)st[j + 2], (uint32_t)st[j + 3], yl);
-        mat4_half((uint32_t)(st[j] >> 32), (uint32_t)(st[j + 1] >> 32), (uint32_t)(st[j + 2] >> 32),
-                  (uint32_t)(st[j + 3] >> 32), yh);
+        uint64_t zl[4], zh[4], yl[4], yh[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            uint64_t A = yl[k] + sl[k], B = yh[k] + sh[k];
-            if (ADD_RC) {
+            zl[k] = acc32(sl[k], (uint32_t)st[j + k]);
+            zh[k] = acc32(sh[k], (uint32_t)(st[j + k] >> 32));
+        }
+        mat4_wide(zl, yl);
+        mat4_wide(zh, yh);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint64_t A = yl[k], B = yh[k];
+            if (RC == kRcAll || (RC == kRcLane0 && j + k == 0)) {
                 A = acc32s(A, (uint32_t)rc[j + k]);
                 B = acc32s(B, (uint32_t)(rc[j + k] >> 32));
             }
@@ -145,125 +152,156 @@ __host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_
     }
 }
 
-// One internal round: st0 <- (st0 + rc)^7, then st_i <- sum + V_i st_i.
-// The round sum is formed from 32-bit halves (two 64-bit running sums, one
-// v_mad_u64_u32 per half) and made canonical, sum = s0 + s1 2^32. Lanes then
-// use the cheapest of two kinds of form:
-//  * exact sums of halves A + B 2^32 (A, B below 2^35), reduced once with the
-//    final fold deferred to one shared rare branch:
-//      V = 2, 3, 4:  A = s0 + V x.lo, B = s1 + V x.hi;
-//      V = -v (v = 2, 3, 4): -v x = v ~x - v (eps - 1) with ~x = 2^64 - 1 - x,
-//                    and -v (eps - 1) = (2^32 - 1 - v) 2^32 + 1 + 2v mod p, so
-//                    A = s0 + 1 + 2v + v ~x.lo, B = s1 + 2^32 - 1 - v + v ~x.hi;
-//      V = 2^-k (k = 3, 4, 5): x 2^-k = q - m eps with q = x >> k and
-//                    m = (x mod 2^k) 2^(32-k), and -m 2^32 = ~m 2^32 + 1
-//                    (2^32 eps = -1), so A = s0 + q.lo + m + 1,
-//                    B = s1 + q.hi + ~m (~m = 2^32 - 1 - m);
-//  * single-correction forms on the canonical sum:
-//      V = -2^-k: sum - x 2^-k = (sum + m eps) - q;
-//      V = 2^-32: sum + x 2^-32 = (sum + x.hi) - x.lo eps, where sum + x.hi
-//                 cannot wrap (sum <= p - 1) and x.lo eps < p;
-//      V = 1, 1/2: sum + t with one wrap correction; V = -1/2: gl_sub2.
-template <int K>
-__host__ __device__ __forceinline__ uint64_t lane_inv_pow2(uint64_t SL1, uint64_t SH, uint64_t x, uint64_t& w)
+template <bool ADD_RC>
+__host__ __device__ __forceinline__ void mds_light16(uint64_t* st, const uint64_t* rc)
 {
-    const uint32_t ql = (uint32_t)(x >> K), qh = (uint32_t)(x >> 32) >> K;
+    mds_light16_rc<ADD_RC ? kRcAll : kRcNone>(st, rc);
+}
+
+// One internal round on a state whose word 0 already includes the round's
+// constant: st0 <- st0^7, then st_i <- sum + V_i st_i. The round sum is kept
+// as two 64-bit sums of 32-bit halves, SL + SH 2^32 (one v_mad_u64_u32 per
+// half, never reduced), and every output is an exact sum of halves
+// A + B 2^32 (A, B below 2^38) reduced once, with the final fold of all of
+// them deferred to one shared rare branch. With ~x = 2^64 - 1 - x, q = x >> k
+// and m = (x mod 2^k) 2^(32-k):
+//   V = 1, 2, 3, 4:  A = SL + V x.lo,             B = SH + V x.hi;
+//   V = -v (v = 2, 3, 4): -v x = v ~x - v (eps - 1) and -v (eps - 1) =
+//                    (2^32 - 1 - v) 2^32 + 1 + 2v (mod p), so
+//                    A = SL + 1 + 2v + v ~x.lo,   B = SH + 2^32 - 1 - v + v ~x.hi;
+//   V = 2^-k (k = 1, 3, 4, 5, 32): x 2^-k = q - m eps = q + m + ~m 2^32 + 1, so
+//                    A = SL + 1 + q.lo + m,       B = SH + q.hi + ~m;
+//   V = -2^-k (k = 1, 3, 4, 5): -x 2^-k = m eps - q = (~m + ~q.lo + 3) +
+//                    (m + ~q.hi - 2) 2^32 (mod p), and ~q.hi - 2 = ~(q.hi + 2), so
+//                    A = SL + 3 + ~m + ~q.lo,     B = SH + m + ~(q.hi + 2);
+//   V = diag15 otherwise: y = x15 diag15, A = SL + y.lo, B = SH + y.hi.
+// The next round's constant rc0_next joins the sums of word 0 (its only
+// use is the next S-box input); the constant parts of the A and B addends
+// are formed on the scalar unit. (Folding the terminal round's constants
+// into all sixteen outputs of the last round as well keeps sixteen more
+// constants live and makes the leaf kernels spill registers.)
+template <int K>
+__host__ __device__ __forceinline__ void inv_pow2_pos(uint64_t x, uint64_t SL, uint64_t SH, uint64_t& A, uint64_t& B)
+{
+    const uint64_t q = x >> K;
     const uint32_t m = (uint32_t)x << (32 - K);
-    const uint64_t A = acc32(acc32(SL1, ql), m);
-    const uint64_t B = acc32(acc32(SH, qh), ~m);
-    return gl_from_halves_defer(A, B, w);
+    A = acc32(acc32(SL + 1, (uint32_t)q), m);
+    B = acc32(acc32(SH, (uint32_t)(q >> 32)), ~m);
+}
+
+template <int K>
+__host__ __device__ __forceinline__ void inv_pow2_neg(uint64_t x, uint64_t SL, uint64_t SH, uint64_t& A, uint64_t& B)
+{
+    const uint64_t q = x >> K;
+    const uint32_t m = (uint32_t)x << (32 - K);
+    A = acc32(acc32(SL + 3, ~m), ~(uint32_t)q);
+    B = acc32(acc32(SH, m), ~((uint32_t)(q >> 32) + 2u));
 }
 
 template <bool DIAG15_IS_INV_2_32>
-__host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t rc, uint64_t diag15)
+__host__ __device__ __forceinline__ void internal_round_core(uint64_t* st, uint64_t rc0_next, uint64_t diag15)
 {
-    uint64_t slo = (uint32_t)st[1], shi = st[1] >> 32;
+    uint64_t SL = (uint32_t)st[1], SH = st[1] >> 32;
 #pragma unroll
     for (int i = 2; i < 16; i++) {
-        slo = acc32(slo, (uint32_t)st[i]);
-        shi = acc32(shi, (uint32_t)(st[i] >> 32));
+        SL = acc32(SL, (uint32_t)st[i]);
+        SH = acc32(SH, (uint32_t)(st[i] >> 32));
     }
-    const uint64_t x0 = sbox7(gl_add_small(st[0], rc));
-    slo = acc32(slo, (uint32_t)x0);
-    shi = acc32(shi, (uint32_t)(x0 >> 32));
-    // sum = slo + shi 2^32 = slo + (shi.lo << 32) + shi.hi 2^64, and 2^64 = eps
-    const uint64_t t = slo + (shi << 32);
-    const uint32_t k = (uint32_t)(shi >> 32) + (t < slo ? 1u : 0u);
-    const uint64_t sum = gl_canon_fast(gl_add_meps_rare(t, k));
-    const uint64_t SL = (uint32_t)sum, SH = sum >> 32;  // the halves of the sum, zero-extended
+    const uint64_t x0 = sbox7(st[0]);
+    SL = acc32(SL, (uint32_t)x0);
+    SH = acc32(SH, (uint32_t)(x0 >> 32));
+    // the constant added to output i: the next round's rc0 on word 0
+    auto cl = [&](int i) -> uint64_t { return i == 0 ? (uint64_t)(uint32_t)rc0_next : 0; };
+    auto ch = [&](int i) -> uint64_t { return i == 0 ? rc0_next >> 32 : 0; };
+    // Each output is finished as soon as its sums are formed (few sums live
+    // at once); the rare final folds are applied per group of four words.
+    uint64_t w[4];
+    auto finish = [&](int i, uint64_t A, uint64_t B) { st[i] = gl_from_halves_defer(A, B, w[i & 3]); };
+    auto fold4 = [&](int j) {
+        const uint64_t any = mask_or(mask_or(w[0], w[1]), mask_or(w[2], w[3]));
+        if (__builtin_expect(any != 0, 0)) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) gl_fold_eps(st[j + i], w[i]);
+        }
+    };
+    uint64_t A, B;
+    {
+        const uint64_t nx = ~x0;  // -2
+        finish(0, acc32m<2>(SL + (5 + cl(0)), (uint32_t)nx), acc32m<2>(SH + (0xFFFFFFFDull + ch(0)), (uint32_t)(nx >> 32)));
+    }
+    finish(1, acc32(SL + cl(1), (uint32_t)st[1]), acc32(SH + ch(1), (uint32_t)(st[1] >> 32)));        //  1
+    finish(2, acc32m<2>(SL + cl(2), (uint32_t)st[2]), acc32m<2>(SH + ch(2), (uint32_t)(st[2] >> 32)));  //  2
+    inv_pow2_pos<1>(st[3], SL + cl(3), SH + ch(3), A, B);                                             //  1/2
+    finish(3, A, B);
+    fold4(0);
+    finish(4, acc32m<3>(SL + cl(4), (uint32_t)st[4]), acc32m<3>(SH + ch(4), (uint32_t)(st[4] >> 32)));  //  3
+    finish(5, acc32m<4>(SL + cl(5), (uint32_t)st[5]), acc32m<4>(SH + ch(5), (uint32_t)(st[5] >> 32)));  //  4
+    inv_pow2_neg<1>(st[6], SL + cl(6), SH + ch(6), A, B);                                             // -1/2
+    finish(6, A, B);
+    {
+        const uint64_t nx = ~st[7];  // -3
+        finish(7, acc32m<3>(SL + (7 + cl(7)), (uint32_t)nx), acc32m<3>(SH + (0xFFFFFFFCull + ch(7)), (uint32_t)(nx >> 32)));
+    }
+    fold4(4);
+    {
+        const uint64_t nx = ~st[8];  // -4
+        finish(8, acc32m<4>(SL + (9 + cl(8)), (uint32_t)nx), acc32m<4>(SH + (0xFFFFFFFBull + ch(8)), (uint32_t)(nx >> 32)));
+    }
+    inv_pow2_pos<3>(st[9], SL + cl(9), SH + ch(9), A, B);  //  1/2^3
+    finish(9, A, B);
+    inv_pow2_pos<4>(st[10], SL + cl(10), SH + ch(10), A, B);  //  1/2^4
+    finish(10, A, B);
+    inv_pow2_pos<5>(st[11], SL + cl(11), SH + ch(11), A, B);  //  1/2^5
+    finish(11, A, B);
+    fold4(8);
+    inv_pow2_neg<3>(st[12], SL + cl(12), SH + ch(12), A, B);  // -1/2^3
+    finish(12, A, B);
+    inv_pow2_neg<4>(st[13], SL + cl(13), SH + ch(13), A, B);  // -1/2^4
+    finish(13, A, B);
+    inv_pow2_neg<5>(st[14], SL + cl(14), SH + ch(14), A, B);  // -1/2^5
+    finish(14, A, B);
+    if (DIAG15_IS_INV_2_32) {
+        // x 2^-32 = x.hi + x.lo + ~x.lo 2^32 + 1 (k = 32: q = x.hi, m = x.lo)
+        const uint64_t x = st[15];
+        finish(15, acc32(acc32(SL + (1 + cl(15)), (uint32_t)(x >> 32)), (uint32_t)x), acc32(SH + ch(15), ~(uint32_t)x));
+    } else {
+        const uint64_t y = gl_mul(st[15], diag15);
+        finish(15, acc32(SL + cl(15), (uint32_t)y), acc32(SH + ch(15), (uint32_t)(y >> 32)));
+    }
+    fold4(12);
+}
 
-    const uint64_t x15 = st[15];
-    uint64_t w[9];
-    {
-        const uint64_t nx = ~x0;                                                              // -2
-        st[0] = gl_from_halves_defer(acc32m<2>(SL + 5, (uint32_t)nx),
-                                     acc32m<2>(SH + 0xFFFFFFFDull, (uint32_t)(nx >> 32)), w[7]);
-    }
-    st[1] = gl_add_small(st[1], sum);                                                         //  1
-    st[2] = gl_from_halves_defer(acc32m<2>(SL, (uint32_t)st[2]), acc32m<2>(SH, (uint32_t)(st[2] >> 32)),
-                                 w[0]);                                                       //  2
-    st[3] = gl_add_small(gl_halve(st[3]), sum);                                               //  1/2
-    st[4] = gl_from_halves_defer(acc32m<3>(SL, (uint32_t)st[4]), acc32m<3>(SH, (uint32_t)(st[4] >> 32)),
-                                 w[1]);                                                       //  3
-    st[5] = gl_from_halves_defer(acc32m<4>(SL, (uint32_t)st[5]), acc32m<4>(SH, (uint32_t)(st[5] >> 32)),
-                                 w[2]);                                                       //  4
-    st[6] = gl_sub2(sum, gl_halve(st[6]));                                                    // -1/2
-    {
-        const uint64_t nx = ~st[7];                                                           // -3
-        st[7] = gl_from_halves_defer(acc32m<3>(SL + 7, (uint32_t)nx),
-                                     acc32m<3>(SH + 0xFFFFFFFCull, (uint32_t)(nx >> 32)), w[3]);
-    }
-    {
-        const uint64_t nx = ~st[8];                                                           // -4
-        st[8] = gl_from_halves_defer(acc32m<4>(SL + 9, (uint32_t)nx),
-                                     acc32m<4>(SH + 0xFFFFFFFBull, (uint32_t)(nx >> 32)), w[8]);
-    }
-    const uint64_t SL1 = SL + 1;
-    st[9] = lane_inv_pow2<3>(SL1, SH, st[9], w[4]);                                           //  1/2^3
-    st[10] = lane_inv_pow2<4>(SL1, SH, st[10], w[5]);                                         //  1/2^4
-    st[11] = lane_inv_pow2<5>(SL1, SH, st[11], w[6]);                                         //  1/2^5
-    st[12] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[12] << 29), st[12] >> 3);            // -1/2^3
-    st[13] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[13] << 28), st[13] >> 4);            // -1/2^4
-    st[14] = gl_sub_small(gl_add_meps(sum, (uint32_t)st[14] << 27), st[14] >> 5);            // -1/2^5
-    if (DIAG15_IS_INV_2_32)
-        st[15] = gl_sub_small(acc32(sum, (uint32_t)(x15 >> 32)), (uint64_t)(uint32_t)x15 * EPS);
-    else
-        st[15] = gl_add_small(gl_mul(x15, diag15), sum);
-    const uint64_t any = mask_or(mask_or(mask_or(w[0], w[1]), mask_or(w[2], w[3])),
-                                 mask_or(mask_or(w[4], w[5]), mask_or(mask_or(w[6], w[7]), w[8])));
-    if (__builtin_expect(any != 0, 0)) {
-        gl_fold_eps(st[0], w[7]);
-        gl_fold_eps(st[8], w[8]);
-        gl_fold_eps(st[2], w[0]);
-        gl_fold_eps(st[4], w[1]);
-        gl_fold_eps(st[5], w[2]);
-        gl_fold_eps(st[7], w[3]);
-        gl_fold_eps(st[9], w[4]);
-        gl_fold_eps(st[10], w[5]);
-        gl_fold_eps(st[11], w[6]);
-    }
+// One internal round as a unit: st0 <- (st0 + rc)^7, then st_i <- sum + V_i st_i.
+template <bool DIAG15_IS_INV_2_32>
+__host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t rc, uint64_t diag15)
+{
+    st[0] = gl_add_small(st[0], rc);
+    internal_round_core<DIAG15_IS_INV_2_32>(st, 0, diag15);
 }
 
 template <bool DIAG15_IS_INV_2_32>
 __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts& C)
 {
     // Initial linear layer fused with the first round's constants.
-    mds_light16<true>(st, C.ext[0]);
+    mds_light16_rc<kRcAll>(st, C.ext[0]);
 #pragma unroll 1
     for (int r = 0; r < 8; r++) {
 #pragma unroll
         for (int i = 0; i < 16; i += 2) sbox7_2(st[i], st[i + 1]);
         if (r == 3) {
-            mds_light16<false>(st, nullptr);
+            // the linear layer adds the first internal round's constant to
+            // word 0 and every internal round the next one's
+            mds_light16_rc<kRcLane0>(st, C.internal);
 #pragma unroll 1
-            for (int k = 0; k < 22; k++) internal_round<DIAG15_IS_INV_2_32>(st, C.internal[k], C.diag15);
-            // Constants of the first terminal round (st += rc) before its S-box.
+            for (int k = 0; k < 22; k++)
+                internal_round_core<DIAG15_IS_INV_2_32>(st, k < 21 ? C.internal[k + 1] : 0, C.diag15);
+            // constants of the first terminal round (st += rc) before its S-box
 #pragma unroll
             for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
         } else if (r == 7) {
-            mds_light16<false>(st, nullptr);
+            mds_light16_rc<kRcNone>(st, nullptr);
         } else {
-            mds_light16<true>(st, C.ext[r + 1]);
+            mds_light16_rc<kRcAll>(st, C.ext[r + 1]);
         }
     }
 }
