@@ -94,6 +94,9 @@ def parse():
                          "copy kernel of known size for scaling rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--valu-peak", action="store_true",
                     help="only run the VALU issue-rate probe (every kind) and print its JSON")
+    ap.add_argument("--copy-ceiling", action="store_true",
+                    help="only time plain device-to-device copies and fills of 8 GiB (the practical "
+                         "HBM ceiling of a streaming kernel) and print their JSON")
     ap.add_argument("--probe-ms", type=float, default=60.0,
                     help="approximate duration of each probe launch")
     ap.add_argument("--ingest-counters", metavar="DIR",
@@ -180,6 +183,31 @@ def valu_probe(kinds, target_ms: float = 60.0):
 
 # ---------------------------------------------------------------------------
 # CPU baseline.
+
+def copy_ceiling(gib: int = 8, reps: int = 5):
+    """HBM rate of the runtime's own device-to-device copy (reads and writes
+    `gib` GiB) and fill (writes `gib` GiB), the practical ceilings of a
+    streaming kernel with a 1:1 and a write-only mix; host clock around
+    `reps` synchronous repetitions after one untimed."""
+    from zkie_amd import _native as N
+    from zkie_amd._native import DeviceBuffer
+    L = N.load()
+    nbytes = gib << 30
+    src, dst = DeviceBuffer(nbytes // 8), DeviceBuffer(nbytes // 8)
+    res = {}
+    for name, fn, moved in (("copy", lambda: L.zkie_memcpy_dtod(dst.addr, src.addr, nbytes, None), 2 * nbytes),
+                            ("fill", lambda: L.zkie_memset(dst.addr, 0, nbytes), nbytes)):
+        N.check(fn(), name)
+        N.check(L.zkie_device_synchronize(), "sync")
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            N.check(fn(), name)
+        N.check(L.zkie_device_synchronize(), "sync")
+        dt = (time.perf_counter() - t0) / reps
+        res[name] = {"bytes": moved, "ms": dt * 1e3, "GB_per_s": moved / dt / 1e9,
+                     "frac_of_8TBps": moved / dt / 8e12}
+    return res
+
 
 def cpu_model() -> str:
     try:
@@ -348,6 +376,9 @@ def main():
     if args.valu_peak:
         res = valu_probe(range(len(PROBE_KINDS)), args.probe_ms)
         print(json.dumps({"valu_issue_rates": list(res.values()), "cus": CUS, "clock_hz": CLOCK_HZ}), flush=True)
+        return
+    if args.copy_ceiling:
+        print(json.dumps({"copy_ceiling": copy_ceiling()}), flush=True)
         return
 
     from zkie_amd import _native as N
