@@ -152,6 +152,22 @@ int zkie_merkle_commit(const uint64_t *d_mat, uint64_t h, uint64_t w, uint64_t *
 int zkie_lde_commit(const uint64_t *d_in, uint64_t h, uint64_t w, uint32_t log_blowup,
                     uint64_t shift, uint64_t *d_out, uint64_t *d_layers, uint64_t *root,
                     void *stream);
+/* Whir::commit_batch (crates/zkie-core/src/pcs/whir.rs:476-525): `count`
+ * tables of 2^arity evaluations each (device pointers, host array d_tables)
+ * stacked table-major into one witness of total_vars = ceil(log2(count
+ * 2^arity)) variables, zero-padded: entry j of table i is entry i 2^arity + j.
+ * The witness, viewed as 2^(total_vars - log_width) rows of 2^log_width, is
+ * committed as by zkie_lde_commit (shift 1). d_stack (2^total_vars u64) holds
+ * the stacked witness on return, except that with log_blowup >= 1 the zero
+ * rows past the tables are neither written nor read; a table already at its
+ * place in d_stack is not copied, one overlapping another part of it is
+ * refused. d_codeword holds 2^(total_vars - log_width + log_blowup) rows;
+ * d_layers and root as for zkie_merkle_commit. The stacking order follows
+ * the layout the reference hands to its external initial-round committer
+ * (p3-whir adapter.rs:106-113); total_vars >= log_width. */
+int zkie_commit_batch(const uint64_t *const *d_tables, uint32_t count, uint32_t arity,
+                      uint32_t log_width, uint32_t log_blowup, uint64_t *d_stack,
+                      uint64_t *d_codeword, uint64_t *d_layers, uint64_t *root, void *stream);
 /* Mmcs::open_batch (p3-merkle-tree mmcs/batch.rs:75-121) for n indices at
  * once: rows_out (host, n*w u64) receives the opened rows, siblings_out
  * (host, n*(num_layers-1)*8 u64) the authentication paths, bottom-up. */

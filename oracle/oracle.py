@@ -168,6 +168,36 @@ def lde_batch(mat: np.ndarray, log_blowup: int, shift: int = 1) -> np.ndarray:
     return out
 
 
+def stack_tables(tables, log_width: int) -> np.ndarray:
+    """The witness of Whir::commit_batch (crates/zkie-core/src/pcs/whir.rs:
+    476-525): same-size tables of 2^arity entries, table-major (entry j of
+    table i at i 2^arity + j), zero-padded to 2^total_vars entries with
+    total_vars = ceil(log2(count 2^arity)), as rows of 2^log_width. The order
+    is the one the reference hands to its external initial-round layout
+    (p3-whir adapter.rs:106-113, MyLayout::new_witness): parity unpinned."""
+    flat = [u64(t).reshape(-1) for t in tables]
+    if not flat:
+        raise ValueError("batch must not be empty")
+    size = flat[0].size
+    if size & (size - 1) or any(t.size != size for t in flat):
+        raise ValueError("all tables must hold the same power-of-two count")
+    total_vars = (len(flat) * size - 1).bit_length()
+    if total_vars < log_width:
+        raise ValueError("the stacked witness fills no row")
+    out = np.zeros(1 << total_vars, np.uint64)
+    out[:len(flat) * size] = np.concatenate(flat)
+    return out.reshape(-1, 1 << log_width)
+
+
+def commit_batch(tables, log_width: int, log_blowup: int):
+    """Stack, encode (zero-padded DFT, writer.rs:73-85) and commit: returns
+    (stacked witness rows, codeword, layers, root)."""
+    stack = stack_tables(tables, log_width)
+    cw = lde_batch(stack, log_blowup)
+    layers, root = merkle_commit(cw)
+    return stack, cw, layers, root
+
+
 # ---- Poseidon2 ---------------------------------------------------------------
 def p2_constants():
     a, b, c, d = (np.zeros(64, np.uint64), np.zeros(64, np.uint64),

@@ -249,8 +249,10 @@ int emu_dft(uint64_t* mat, uint32_t lg, uint64_t w, int inverse, uint32_t thread
     return 0;
 }
 
-int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t* out,
-            uint32_t threads)
+// LDE reading only the first in_rows rows of `in` (the rest are zero
+// coefficients), as the library's batch commit does.
+int emu_lde_rows(const uint64_t* in, uint64_t h, uint64_t in_rows, uint64_t w, uint32_t log_blowup,
+                 uint64_t* out, uint32_t threads)
 {
     uint32_t lgh = 0;
     while ((1ull << lgh) < h) lgh++;
@@ -261,11 +263,17 @@ int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uin
     std::vector<uint64_t> tmp(n * w);
     uint32_t B = L;
     for (uint32_t i = 0; i < p.np; i++) {
-        const PassArgs a = pass_args(p, i, B, w, in, h, tmp.data(), out, tab.data(), false);
+        const PassArgs a = pass_args(p, i, B, w, in, in_rows, tmp.data(), out, tab.data(), false);
         run_pass(a, threads, false);
         B -= a.s;
     }
     return 0;
+}
+
+int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t* out,
+            uint32_t threads)
+{
+    return emu_lde_rows(in, h, h, w, log_blowup, out, threads);
 }
 
 // LDE of 16-wide rows with the last pass fused with the leaf hash: out gets

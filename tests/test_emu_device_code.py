@@ -145,6 +145,19 @@ def test_lde_passes_kernel_threads(emu, oracle, lg, w, lb):
     assert (out == oracle.lde_batch(x, lb)).all()
 
 
+@pytest.mark.parametrize("lg,w,lb,rows", [(10, 16, 2, 300), (13, 16, 2, 5000), (12, 4, 1, 1), (7, 1, 3, 100),
+                                          (5, 16, 2, 17), (12, 16, 2, 3000), (13, 1, 1, 4097)])
+def test_lde_passes_ragged_rows(emu, oracle, lg, w, lb, rows):
+    """The LDE of a batch commit: only the first `rows` input rows exist (the
+    buffer ends there, every read is bounds-checked), the rest are zero."""
+    x = oracle.gen_uniform(9 + rows, rows * w).reshape(rows, w)
+    full = np.zeros((1 << lg, w), np.uint64)
+    full[:rows] = x
+    out = np.zeros(((1 << lg) << lb, w), np.uint64)
+    assert emu.emu_lde_rows(ptr(x), 1 << lg, rows, w, lb, ptr(out), 512) == 0
+    assert (out == oracle.lde_batch(full, lb)).all()
+
+
 @pytest.mark.parametrize("lg,lb", [(8, 2), (10, 2), (12, 2), (11, 3), (13, 3), (16, 2)])
 def test_lde_last_pass_fused_with_leaf_hash(emu, oracle, lg, lb):
     """The fused last NTT pass + leaf hash of the commitment (last_leaf.hpp),

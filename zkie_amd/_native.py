@@ -46,6 +46,7 @@ SIGNATURES = {
     "zkie_merkle_layout": [_u64, _u32p, _u64p],
     "zkie_merkle_commit": [_vp, _u64, _u64, _vp, _u64p, _vp],
     "zkie_lde_commit": [_vp, _u64, _u64, _u32, _u64, _vp, _vp, _u64p, _vp],
+    "zkie_commit_batch": [_u64p, _u32, _u32, _u32, _u32, _vp, _vp, _vp, _u64p, _vp],
     "zkie_merkle_open_batch": [_vp, _u64, _u64, _vp, _u64p, _u64, _u64p, _u64p, _vp],
     "zkie_merkle_open_pruned": [_vp, _u64, _u64, _vp, _u64p, _u64, _u64p, _u64p, _u64, _u64p, _vp],
     "zkie_fold_rows": [_vp, _u64, _u32, _int, _u64p, _vp, _vp],

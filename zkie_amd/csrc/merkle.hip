@@ -543,8 +543,8 @@ int merkle_commit_device(const uint64_t* d_mat, uint64_t h, uint64_t w, uint64_t
 // The LDE of d_in into d_cw followed by the commitment of its rows into
 // d_layers: the last NTT pass hashes the rows it produces when it can
 // (fusable_last_pass), otherwise the leaf kernel hashes the finished codeword.
-int lde_commit_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
-                      uint64_t* d_cw, uint64_t* d_layers, hipStream_t s)
+int lde_commit_device(const uint64_t* d_in, uint64_t h, uint64_t in_rows, uint64_t w, uint32_t log_blowup,
+                      uint64_t shift, uint64_t* d_cw, uint64_t* d_layers, hipStream_t s)
 {
     if (h == 0 || (h & (h - 1)) != 0 || log_blowup > 32 || !d_layers || (w > 0 && (!d_in || !d_cw)))
         return ZKIE_ERR_INVALID;
@@ -558,7 +558,7 @@ int lde_commit_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log
     FuseCtx ctx{d_layers, fast, false};
     const LastPassHook hook{fuse_hook, &ctx};
     if (w > 0) {
-        rc = lde_run(d_in, h, w, log_blowup, shift, d_cw, s, nullptr, &hook);
+        rc = lde_run_rows(d_in, h, in_rows, w, log_blowup, shift, d_cw, s, nullptr, &hook);
         if (rc) return rc;
     }
     const std::vector<uint64_t> lens = layer_lens(n);
@@ -572,6 +572,31 @@ int lde_commit_device(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log
     }
     if (lens.size() == 1) return ZKIE_OK;
     return build_upper(d_layers, lens, fast, s);
+}
+
+// The root of an n-row tree (its last layer) into host memory, after the
+// work queued on s.
+int root_to_host(const uint64_t* d_layers, uint64_t n, uint64_t* root, hipStream_t s)
+{
+    if (!root) return ZKIE_OK;
+    const std::vector<uint64_t> lens = layer_lens(n);
+    uint64_t off = 0;
+    for (size_t i = 0; i + 1 < lens.size(); i++) off += lens[i] * 8;
+    ZK_TRY(hipMemcpyAsync(root, d_layers + off, 64, hipMemcpyDeviceToHost, s));
+    ZK_TRY(hipStreamSynchronize(s));
+    return ZKIE_OK;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(uint64_t* __restrict__ p, uint64_t n)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+unsigned stride_blocks(uint64_t n)
+{
+    const uint64_t g = (n + 255) / 256;
+    return (unsigned)(g < (1ull << 16) ? (g ? g : 1) : (1ull << 16));
 }
 
 }  // namespace zk
@@ -680,16 +705,50 @@ int zkie_lde_commit(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_b
                     uint64_t* d_out, uint64_t* d_layers, uint64_t* root, void* stream)
 {
     hipStream_t s = as_stream(stream);
-    int rc = lde_commit_device(d_in, h, w, log_blowup, shift, d_out, d_layers, s);
+    int rc = lde_commit_device(d_in, h, h, w, log_blowup, shift, d_out, d_layers, s);
     if (rc) return rc;
-    if (root) {
-        const std::vector<uint64_t> lens = layer_lens(h << log_blowup);
-        uint64_t off = 0;
-        for (size_t i = 0; i + 1 < lens.size(); i++) off += lens[i] * 8;
-        ZK_TRY(hipMemcpyAsync(root, d_layers + off, 64, hipMemcpyDeviceToHost, s));
-        ZK_TRY(hipStreamSynchronize(s));
+    return root_to_host(d_layers, h << log_blowup, root, s);
+}
+
+int zkie_commit_batch(const uint64_t* const* d_tables, uint32_t count, uint32_t arity, uint32_t log_width,
+                      uint32_t log_blowup, uint64_t* d_stack, uint64_t* d_codeword, uint64_t* d_layers,
+                      uint64_t* root, void* stream)
+{
+    if (!d_tables || count == 0 || arity > 40 || log_width > 16 || !d_stack || !d_codeword || !d_layers)
+        return ZKIE_ERR_INVALID;
+    const uint64_t len = 1ull << arity;
+    const uint64_t total = (uint64_t)count << arity;
+    uint32_t vars = 0;  // total_num_vars: the stacked witness has 2^vars entries
+    while ((1ull << vars) < total) vars++;
+    if (vars < log_width || vars - log_width + log_blowup > 32) return ZKIE_ERR_INVALID;
+    const uint64_t w = 1ull << log_width;
+    const uint64_t h = 1ull << (vars - log_width);
+    // rows holding table entries; with no blowup every row is read, so the
+    // zero padding is written out
+    const uint64_t data_rows = log_blowup ? (total + w - 1) / w : h;
+    const uint64_t end = data_rows * w;
+    // A table already in its slot of the stack is not copied; one that
+    // overlaps any other part of the stack would be overwritten while read.
+    const uintptr_t s0 = (uintptr_t)d_stack, s1 = s0 + end * 8;
+    for (uint32_t i = 0; i < count; i++) {
+        const uint64_t* t = d_tables[i];
+        if (!t) return ZKIE_ERR_INVALID;
+        if (t == d_stack + (uint64_t)i * len) continue;
+        const uintptr_t t0 = (uintptr_t)t, t1 = t0 + len * 8;
+        if (t0 < s1 && s0 < t1) return ZKIE_ERR_INVALID;
     }
-    return ZKIE_OK;
+    hipStream_t s = as_stream(stream);
+    for (uint32_t i = 0; i < count; i++) {
+        if (d_tables[i] == d_stack + (uint64_t)i * len) continue;
+        ZK_TRY(hipMemcpyAsync(d_stack + (uint64_t)i * len, d_tables[i], len * 8, hipMemcpyDeviceToDevice, s));
+    }
+    if (end > total) {
+        zero_kernel<<<stride_blocks(end - total), 256, 0, s>>>(d_stack + total, end - total);
+        ZK_LAUNCHED();
+    }
+    const int rc = lde_commit_device(d_stack, h, data_rows, w, log_blowup, 1, d_codeword, d_layers, s);
+    if (rc) return rc;
+    return root_to_host(d_layers, h << log_blowup, root, s);
 }
 
 namespace {

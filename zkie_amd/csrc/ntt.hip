@@ -274,10 +274,14 @@ int dft_inplace(uint64_t* d_mat, uint64_t* d_tmp, uint32_t lg, uint64_t w, bool 
 
 }  // namespace
 
-int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
-            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws, const LastPassHook* hook)
+int lde_run_rows(const uint64_t* d_in, uint64_t h, uint64_t in_rows, uint64_t w, uint32_t log_blowup,
+                 uint64_t shift, uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws,
+                 const LastPassHook* hook)
 {
     if (h == 0 || (h & (h - 1)) != 0 || !d_in || !d_out) return ZKIE_ERR_INVALID;
+    // A first pass that reads fewer rows than its tile covers prunes inputs
+    // of a step-0 radix below 8; with no blowup every input can be non-zero.
+    if (in_rows == 0 || in_rows > h || (in_rows < h && log_blowup == 0)) return ZKIE_ERR_INVALID;
     uint32_t lgh = 0;
     while ((1ull << lgh) < h) lgh++;
     const uint32_t L = lgh + log_blowup;
@@ -296,7 +300,8 @@ int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, u
         auto scale = [&](uint64_t* d_tab) -> int {
             coset_tables_kernel<<<(unsigned)(kBigLen / 256), 256, 0, s>>>(shift, d_tab, d_tab + kBigLen);
             ZK_LAUNCHED();
-            coset_scale_kernel<<<stride_grid(h * w), 256, 0, s>>>(d_in, d_out, h, w, d_tab, d_tab + kBigLen);
+            coset_scale_kernel<<<stride_grid(in_rows * w), 256, 0, s>>>(d_in, d_out, in_rows, w, d_tab,
+                                                                       d_tab + kBigLen);
             ZK_LAUNCHED();
             return ZKIE_OK;
         };
@@ -313,15 +318,15 @@ int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, u
     }
     if (p.np == 1) {
         if (src == d_out) {
-            // in place, single pass: rows >= h are treated as zero
-            return run_passes(p, w, d_out, h, nullptr, d_out, false, s);
+            // in place, single pass: rows >= in_rows are treated as zero
+            return run_passes(p, w, d_out, in_rows, nullptr, d_out, false, s);
         }
-        return run_passes(p, w, src, h, nullptr, d_out, false, s);
+        return run_passes(p, w, src, in_rows, nullptr, d_out, false, s);
     }
-    if (ws) return run_passes(p, w, src, h, ws->ntt, d_out, false, s, hook);
+    if (ws) return run_passes(p, w, src, in_rows, ws->ntt, d_out, false, s, hook);
     Scratch lease(WS_NTT, n * w * 8, s);
     if (lease.status()) return lease.status();
-    return run_passes(p, w, src, h, (uint64_t*)lease.get(), d_out, false, s, hook);
+    return run_passes(p, w, src, in_rows, (uint64_t*)lease.get(), d_out, false, s, hook);
 }
 
 // Exposed to the other translation units of the library.

@@ -93,8 +93,17 @@ struct LastPassHook {
 };
 
 // zkie_lde_batch with the work buffers of `ws`, or leased ones when ws is
-// null; `hook` (may be null) is offered the last pass.
-int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
-            uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws, const LastPassHook* hook);
+// null; `hook` (may be null) is offered the last pass. Only the first
+// in_rows (1 <= in_rows <= h) rows of d_in are read: the rows from in_rows to
+// h are zero coefficients. in_rows < h needs log_blowup >= 1.
+int lde_run_rows(const uint64_t* d_in, uint64_t h, uint64_t in_rows, uint64_t w, uint32_t log_blowup,
+                 uint64_t shift, uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws,
+                 const LastPassHook* hook);
+
+inline int lde_run(const uint64_t* d_in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t shift,
+                   uint64_t* d_out, hipStream_t s, const LdeWorkspace* ws, const LastPassHook* hook)
+{
+    return lde_run_rows(d_in, h, h, w, log_blowup, shift, d_out, s, ws, hook);
+}
 
 }  // namespace zk

@@ -130,6 +130,32 @@ class HipMerkleTreeMmcs:
                                         N.p(root), stream), "zkie_lde_commit")
         return HipMerkleTree(d_codeword, n, w, d_layers, root)
 
+    def commit_batch_device(self, tables, arity: int, log_width: int, log_blowup: int,
+                            d_stack: DeviceBuffer | None = None,
+                            stream=None) -> tuple[HipMerkleTree, DeviceBuffer]:
+        """Whir::commit_batch (whir.rs:476-525) on device tables of 2^arity
+        entries each: stacked table-major into d_stack (2^total_vars entries,
+        total_vars = ceil(log2(len(tables) 2^arity))), viewed as rows of
+        2^log_width, encoded and committed. Returns the tree of the codeword
+        and the stack."""
+        count = len(tables)
+        if count == 0:
+            raise ValueError("batch must not be empty")
+        total_vars = ((count << arity) - 1).bit_length()
+        if total_vars < log_width:
+            raise ValueError(f"{count} tables of 2^{arity} entries fill no row of 2^{log_width}")
+        if d_stack is None:
+            d_stack = DeviceBuffer(1 << total_vars)
+        n = 1 << (total_vars - log_width + log_blowup)
+        d_codeword = DeviceBuffer(n << log_width)
+        d_layers = DeviceBuffer(sum(N.merkle_layout(n)) * 8)
+        ptrs = np.array([t.addr for t in tables], np.uint64)
+        root = np.zeros(8, np.uint64)
+        check(N.load().zkie_commit_batch(N.p(ptrs), count, arity, log_width, log_blowup, d_stack.addr,
+                                         d_codeword.addr, d_layers.addr, N.p(root), stream),
+              "zkie_commit_batch")
+        return HipMerkleTree(d_codeword, n, 1 << log_width, d_layers, root), d_stack
+
     def commit(self, mat) -> tuple[np.ndarray, HipMerkleTree]:
         m = _as_matrix(mat)
         h, w = m.shape
