@@ -80,7 +80,7 @@ def parse():
     ap.add_argument("--no-fuse", action="store_true",
                     help="commit with separate zkie_lde_batch and zkie_merkle_commit calls (the leaf "
                          "kernel re-reads the codeword) instead of zkie_lde_commit")
-    ap.add_argument("--cpu-rows", type=int, default=1 << 21,
+    ap.add_argument("--cpu-rows", type=int, default=1 << 23,
                     help="coefficient rows of the CPU baseline sample")
     ap.add_argument("--prover-data", action="store_true",
                     help="after the timed steps, also time streaming the committed tree out of "
@@ -109,12 +109,16 @@ def parse():
 # ---------------------------------------------------------------------------
 # Kernel sources and the counter profile measured on them.
 
+# Translation units whose kernels the step launches (every header counts).
+STEP_SOURCES = ("runtime.hip", "ntt.hip", "merkle.hip", "fold.hip")
+
+
 def source_hash() -> str:
-    """Hash of the kernel sources: a counter profile is valid only for the
-    code it was measured on."""
+    """Hash of the step's kernel sources: a counter profile is valid only for
+    the code it was measured on."""
     h = hashlib.sha256()
     for path in sorted(glob.glob(os.path.join(ROOT, "zkie_amd", "csrc", "*"))):
-        if path.endswith((".hip", ".hpp")) and not path.endswith("valu_probe.hip"):
+        if path.endswith(".hpp") or os.path.basename(path) in STEP_SOURCES:
             h.update(os.path.basename(path).encode())
             with open(path, "rb") as f:
                 h.update(f.read())
