@@ -104,7 +104,7 @@ void run_pass_inv(const PassArgs& a, uint32_t T)
 template <int S>
 void run_last_leaf_s(const PassArgs& a, uint64_t* digests, uint64_t digests_len, const P2Consts& C, bool d15)
 {
-    constexpr uint32_t T = 256;
+    constexpr uint32_t T = fuse_threads<S>();
     using LL = LastLeaf<S>;
     const uint64_t blocks = pass_blocks(a);
     std::vector<uint64_t> lds(LL::lds_words());

@@ -32,19 +32,24 @@ def restated():
     }
 
 
-def main(path):
-    got = json.load(open(path))
+def compare(got) -> int:
+    """Print one line per field of the restatement; return the number of
+    fields that differ or are missing."""
     want = restated()
     bad = 0
     for key, exp in want.items():
         if key not in got:
-            print(f"{key}: missing from {path}")
+            print(f"{key}: missing")
             bad += 1
             continue
         ok = got[key] == exp
         bad += not ok
         print(f"{key}: {'same' if ok else 'DIFFERENT'}")
-    sys.exit(1 if bad else 0)
+    return bad
+
+
+def main(path):
+    sys.exit(1 if compare(json.load(open(path))) else 0)
 
 
 if __name__ == "__main__":

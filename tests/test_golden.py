@@ -120,3 +120,10 @@ def test_reference_comparison_script_matches_the_oracle(oracle):
     assert [int(x, 16) for x in w["two_adic_generators"]] == [oracle.two_adic_generator(k) for k in range(33)]
     iota = np.arange(16, dtype=np.uint64)
     assert [int(x, 16) for x in w["p2_permute_iota"]] == [int(x) for x in oracle.p2_permute(iota)]
+    # the restatement compares equal to itself, and a single planted
+    # difference (one diagonal word) or a missing field is reported
+    assert cra.compare(w) == 0
+    planted = dict(w, matrix_diag_16=list(w["matrix_diag_16"]))
+    planted["matrix_diag_16"][7] = f"{(int(planted['matrix_diag_16'][7], 16) + 1) % (2**64):016x}"
+    assert cra.compare(planted) == 1
+    assert cra.compare({k: v for k, v in w.items() if k != "ext_w"}) == 1

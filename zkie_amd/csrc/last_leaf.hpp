@@ -23,6 +23,15 @@ namespace zk {
 
 constexpr int kFuseLogV = 4;  // 16 columns of one j2
 
+// Threads of a fused workgroup: one per row of the tile (every lane hashes
+// in the last phase, which holds most of the work), at least one wave. With
+// one row per thread the last step keeps at most 16 outputs per thread.
+template <int S>
+__host__ __device__ constexpr uint32_t fuse_threads()
+{
+    return S <= 6 ? 64u : (1u << S);
+}
+
 template <int S>
 struct LastLeaf {
     using Rd = Radix<S>;

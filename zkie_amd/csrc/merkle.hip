@@ -203,14 +203,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
 // The last pass of a 16-wide LDE fused with the leaf hash (last_leaf.hpp):
 // one workgroup per tile of the pass, 256 threads (four workgroups per CU
 // for tiles of up to 256 rows).
-constexpr uint32_t kFuseThreads = 256;
 
 template <int S, bool D15>
-__global__ __launch_bounds__(kFuseThreads) __attribute__((amdgpu_waves_per_eu(4))) void ntt_last_leaf_kernel(
+__global__ __launch_bounds__(fuse_threads<S>()) __attribute__((amdgpu_waves_per_eu(4))) void ntt_last_leaf_kernel(
     PassArgs a, uint64_t* __restrict__ digests)
 {
     extern __shared__ uint64_t lds[];
-    constexpr uint32_t T = kFuseThreads;
+    constexpr uint32_t T = fuse_threads<S>();
     const uint32_t tid = threadIdx.x;
     __builtin_assume(tid < T);
     const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
@@ -478,7 +477,7 @@ hipError_t launch_last_leaf_s(const PassArgs& a, uint64_t* digests, hipStream_t 
         if ((blocks % 65536) != 0) return hipErrorInvalidValue;
         grid = dim3(65536u, (unsigned)(blocks / 65536), 1);
     }
-    ntt_last_leaf_kernel<S, D15><<<grid, kFuseThreads, shmem, s>>>(a, digests);
+    ntt_last_leaf_kernel<S, D15><<<grid, fuse_threads<S>(), shmem, s>>>(a, digests);
     return hipGetLastError();
 }
 
