@@ -286,10 +286,10 @@ def sumcheck_rounds(N, stream, t: int = 22, k: int = 4, reps: int = 20):
     """Time zkie_sumcheck_prove: k rounds over a base table of 2^t entries
     times an EF weight table (the first round of the opening-pipeline
     workload), per kernel with the library's HIP-event timers. Algorithmic
-    bytes: round 0's sums read both tables (f: 8 B per base entry, h: 16 B),
-    then every round's fold reads both tables (f: 8 B in round 0, then 16 B
-    EF) and writes the two halved EF tables, the folds before the last one
-    forming the next round's sums in the same pass."""
+    bytes: both tables read once (f: 8 B per base entry, h: 16 B) and the two
+    folded EF tables of 2^(t - k) entries written. The library runs the
+    rounds in passes (two rounds per pass on tables of 2^20 entries or more,
+    up to four otherwise); pass_bytes is what those passes move."""
     import numpy as np
 
     from zkie_amd import configs as C
@@ -307,18 +307,19 @@ def sumcheck_rounds(N, stream, t: int = 22, k: int = 4, reps: int = 20):
     for _ in range(reps):
         sumcheck_prove(d_f, False, d_h, t, r, stream.handle)
     dt = (time.perf_counter() - t0) / reps
-    kern = {name: N.profile_query(name) for name in ("sumcheck_round", "sumcheck_fold_round", "sumcheck_fold",
-                                                  "sumcheck_finish")}
+    kern = {name: N.profile_query(name) for name in ("sumcheck_pass", "sumcheck_finish")}
     N.profile_enable(False)
-    alg = (1 << t) * (8 + 16)
-    for i in range(k):
+    alg = (1 << t) * (8 + 16) + (1 << (t - k)) * 32
+    pass_bytes, i = 0, 0
+    while i < k:
         m = t - i
-        fb = 8 if i == 0 else 16
-        alg += (1 << m) * (fb + 16) + (1 << (m - 1)) * 32
+        kk = min(2 if m >= 20 else 4, k - i)
+        pass_bytes += (1 << m) * ((8 if i == 0 else 16) + 16) + (1 << (m - kk)) * 32
+        i += kk
     dev_ms = sum(ms for _, ms in kern.values()) / reps
     return {"table": f"2^{t} base x EF weights", "rounds": k, "ms_per_call": round(dt * 1e3, 3),
-            "kernel_ms_per_call": round(dev_ms, 3), "alg_bytes": alg,
-            "GB_per_s_kernels": round(alg / (dev_ms * 1e-3) / 1e9, 1) if dev_ms else None,
+            "kernel_ms_per_call": round(dev_ms, 3), "alg_bytes": alg, "pass_bytes": pass_bytes,
+            "GB_per_s_kernels": round(pass_bytes / (dev_ms * 1e-3) / 1e9, 1) if dev_ms else None,
             "hbm_frac_kernels": round(alg / (dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if dev_ms else None,
             "per_kernel_avg_ms": {n_: round(ms / max(c, 1), 4) for n_, (c, ms) in kern.items()}}
 

@@ -13,7 +13,7 @@ using namespace zk;
 
 namespace {
 
-constexpr int kOps = 11;
+constexpr int kOps = 16;
 
 __global__ void binary_kernel(const uint64_t* a, const uint64_t* b, uint64_t* out, uint64_t n)
 {
@@ -37,6 +37,13 @@ __global__ void binary_kernel(const uint64_t* a, const uint64_t* b, uint64_t* ou
     gl_mul2(x, y, x, x, p, q);  // two different products through the interleaved form
     o[9] = gl_canon(p);
     o[10] = gl_canon(q);
+    o[11] = gl_canon(gl_mul7(x));
+    const Ef e = ef_mul(Ef{x, y}, Ef{y, x});  // (x + y X)(y + x X) in F[X]/(X^2 - 7)
+    o[12] = gl_canon(e.c0);
+    o[13] = gl_canon(e.c1);
+    const Ef eb = ef_mul_base(Ef{x, y}, y);
+    o[14] = gl_canon(eb.c0);
+    o[15] = gl_canon(eb.c1);
 }
 
 // st: n states of 16 words; mode 0 mds_light16, 1 internal round (rc, diag15

@@ -72,7 +72,8 @@ def test_binary_ops_on_edges_and_random(native):
     i24 = pow(1 << 24, P - 2, P)
     for n, (x, y) in enumerate(pairs):
         want = [(x + y) % P, (x - y) % P, x * y % P, x * x % P, (x << 24) % P, (x << 48) % P, x * i24 % P,
-                ((x >> 29) + ((y >> 29) << 32)) % P, ((x >> 29) + ((y >> 29) << 32)) % P, x * y % P, x * x % P]
+                ((x >> 29) + ((y >> 29) << 32)) % P, ((x >> 29) + ((y >> 29) << 32)) % P, x * y % P, x * x % P,
+                7 * x % P, 8 * x * y % P, (x * x + y * y) % P, x * y % P, y * y % P]
         got = [int(v) for v in out[n]]
         assert got == want, (hex(x), hex(y), got, want)
 

@@ -9,9 +9,12 @@
 //          c2 = (y2 - 2 y1 + y0) / 2;
 //   fold:  b[s] = a[2s] + r (a[2s + 1] - a[2s]) for both tables.
 // f is base or EF, h and every folded table EF = F[x]/(x^2 - 7) flattened
-// [c0, c1]; challenges are EF. Both kernels stream their tables once
-// (HBM-bound): the round kernel reduces its three EF sums per workgroup in
-// LDS and one small workgroup adds the partial sums.
+// [c0, c1]; challenges are EF. The round-by-round entry points (the
+// interactive form: each challenge drawn from the previous round's message)
+// stream the tables once per round, the round kernel reducing its three EF
+// sums per workgroup in LDS and one small workgroup adding the partial sums.
+// zkie_sumcheck_prove, whose challenges are all given (sumcheck.rs:33-38),
+// runs several rounds per pass over the tables (sc_multi_kernel).
 #include <algorithm>
 #include <vector>
 
@@ -194,6 +197,93 @@ __global__ __launch_bounds__(kScThreads) void sc_fold_round_kernel(const uint64_
     if (threadIdx.x == 0) {
 #pragma unroll
         for (int e = 0; e < 6; e++) partial[6 * (uint64_t)blockIdx.x + e] = gl_canon(v[e]);
+    }
+}
+
+// ---- several rounds in one pass (challenges known in advance) --------------
+// sumcheck::prove takes all its challenges at once (sumcheck.rs:33-38), so K
+// consecutive rounds need no reduction between them: the entries of a block
+// of 2^K consecutive indices pair up in round 1 (bit 0), their folds pair up
+// in round 2 (bit 1), and so on, and the whole tree of one block is formed in
+// registers. Each lane takes whole blocks, adds every pair's products to its
+// round's three sums, and writes the block's fully folded entry of both
+// tables; the tables are streamed once for K rounds.
+constexpr int kScMultiMax = 4;  // rounds per pass
+// Rounds of a pass over a table of 2^m entries: four rounds in one pass keep
+// a 16-entry tree per lane (about 110 VGPRs, four waves per SIMD), which
+// is latency-bound on large tables; there two passes of two rounds stream
+// faster (2^22 base entries x EF weights, 4 rounds: 89 us against 112 us of
+// kernel time), while small tables are bound by the launches.
+constexpr uint32_t kScWideLog = 20;
+uint32_t sc_pass_rounds(uint32_t m, uint32_t left)
+{
+    return std::min<uint32_t>(m >= kScWideLog ? 2 : kScMultiMax, left);
+}
+
+struct ScChallenges {
+    uint64_t r[2 * kScMultiMax];  // EF challenges of the pass's rounds, canonical
+};
+
+// The folded entry of the 2^J-entry sub-block at `off`, adding the products
+// of its rounds 1..J (tree order) to acc[0..J). BASE: f entries of the block
+// are base-field values (f not EF and J = 1, so both pair members are loads).
+template <bool FEXT, int J, int K>
+__device__ __forceinline__ void sc_tree(const uint64_t* __restrict__ f, const uint64_t* __restrict__ h,
+                                        uint64_t off, const ScChallenges& c, Ef (&acc)[K][3], Ef& fo, Ef& ho)
+{
+    if constexpr (J == 0) {
+        fo = sc_load_f<FEXT>(f, off);
+        ho = Ef{h[2 * off], h[2 * off + 1]};
+    } else {
+        Ef fa, ha, fb, hb;
+        sc_tree<FEXT, J - 1, K>(f, h, off, c, acc, fa, ha);
+        sc_tree<FEXT, J - 1, K>(f, h, off + (1ull << (J - 1)), c, acc, fb, hb);
+        constexpr bool BASE = !FEXT && J == 1;
+        const Ef r{c.r[2 * (J - 1)], c.r[2 * (J - 1) + 1]};
+        const Ef f2 = ef_sub(ef_add(fb, fb), fa), h2 = ef_sub(ef_add(hb, hb), ha);
+        acc[J - 1][0] = ef_add(acc[J - 1][0], sc_mul<!BASE>(fa, ha));
+        acc[J - 1][1] = ef_add(acc[J - 1][1], sc_mul<!BASE>(fb, hb));
+        acc[J - 1][2] = ef_add(acc[J - 1][2], sc_mul<!BASE>(f2, h2));
+        const Ef df = ef_sub(fb, fa);
+        fo = ef_add(fa, BASE ? ef_mul_base(r, df.c0) : ef_mul(r, df));
+        ho = ef_add(ha, ef_mul(r, ef_sub(hb, ha)));
+    }
+}
+
+// K rounds over tables of nblk 2^K entries: the folded tables (nblk EF
+// entries each) and, per round j, one record of its three EF sums per
+// workgroup at partial + 6 (j kScMaxBlocks + workgroup).
+template <bool FEXT, int K>
+__global__ __launch_bounds__(kScThreads) void sc_multi_kernel(const uint64_t* __restrict__ f,
+                                                              const uint64_t* __restrict__ h, uint64_t nblk,
+                                                              const ScChallenges c, uint64_t* __restrict__ f_out,
+                                                              uint64_t* __restrict__ h_out,
+                                                              uint64_t* __restrict__ partial)
+{
+    __shared__ uint64_t red[6][kScThreads];
+    Ef acc[K][3];
+#pragma unroll
+    for (int j = 0; j < K; j++)
+#pragma unroll
+        for (int e = 0; e < 3; e++) acc[j][e] = Ef{0, 0};
+    const uint64_t stride = (uint64_t)gridDim.x * kScThreads;
+    for (uint64_t b = (uint64_t)blockIdx.x * kScThreads + threadIdx.x; b < nblk; b += stride) {
+        Ef fo, ho;
+        sc_tree<FEXT, K, K>(f, h, b << K, c, acc, fo, ho);
+        f_out[2 * b] = gl_canon(fo.c0);
+        f_out[2 * b + 1] = gl_canon(fo.c1);
+        h_out[2 * b] = gl_canon(ho.c0);
+        h_out[2 * b + 1] = gl_canon(ho.c1);
+    }
+#pragma unroll
+    for (int j = 0; j < K; j++) {
+        uint64_t v[6] = {acc[j][0].c0, acc[j][0].c1, acc[j][1].c0, acc[j][1].c1, acc[j][2].c0, acc[j][2].c1};
+        sc_block_reduce(v, red);
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int e = 0; e < 6; e++) partial[6 * ((uint64_t)j * kScMaxBlocks + blockIdx.x) + e] = gl_canon(v[e]);
+        }
+        __syncthreads();  // the reduction area is reused by the next round
     }
 }
 
@@ -549,11 +639,14 @@ int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, 
         return ZKIE_OK;
     }
     // Workspace: partial sums, then every round's y sums (6 u64 each), then
-    // the folded tables of the intermediate rounds: even rounds write region
-    // A (f, h of at most `half` EF entries each: 4 half u64), odd rounds region
-    // B after it (at most half / 2 entries each: 2 half u64).
-    const uint64_t half = n >> 1;
-    const uint64_t pool_u64 = rounds > 1 ? 6 * half : 0;
+    // the folded tables between passes: even passes write region A (f and h
+    // of the first pass's output size, EF), odd passes region B after it
+    // (the second pass's output size); the last pass writes the outputs.
+    const uint32_t k0 = sc_pass_rounds(num_vars, rounds);
+    const uint32_t k1 = rounds > k0 ? sc_pass_rounds(num_vars - k0, rounds - k0) : 0;
+    const uint64_t out_a = rounds > k0 ? n >> k0 : 0;
+    const uint64_t out_b = rounds > k0 + k1 ? n >> (k0 + k1) : 0;
+    const uint64_t pool_u64 = 4 * out_a + 4 * out_b;
     // Every round keeps its own partial records, added by one launch at the end.
     Scratch ws(WS_FOLD, (6 * (kScMaxBlocks + 1) * rounds + pool_u64) * 8, s);
     if (ws.status()) return ws.status();
@@ -564,31 +657,45 @@ int zkie_sumcheck_prove(const uint64_t* d_f, int f_is_ext, const uint64_t* d_h, 
     const uint64_t* cf = d_f;
     const uint64_t* ch = d_h;
     bool ext = f_is_ext != 0;
-    // round 0's sums, then each fold computes the next round's sums in the
-    // same pass; the last fold is a plain one
-    int rc = sc_sums(cf, ext, ch, num_vars, partial, &counts.n[0], s);
-    if (rc) return rc;
-    for (uint32_t i = 0; i < rounds; i++) {
-        const uint32_t m = num_vars - i;
+    // passes of up to kScMultiMax rounds, each streaming the tables once
+    for (uint32_t i = 0, p = 0; i < rounds; p++) {
+        const uint32_t K = sc_pass_rounds(num_vars - i, rounds - i);
+        const uint64_t nblk = 1ull << (num_vars - i - K);
         uint64_t *nf_, *nh_;
-        if (i + 1 == rounds) {
+        if (i + K == rounds) {
             nf_ = d_f_out;
             nh_ = d_h_out;
         } else {
-            // round i writes half >> i EF entries per table
-            uint64_t* base = (i % 2 == 0) ? pool : pool + 4 * half;
+            // passes shrink the table, so later passes fit their region
+            uint64_t* base = (p % 2 == 0) ? pool : pool + 4 * out_a;
             nf_ = base;
-            nh_ = base + (i % 2 == 0 ? 2 * half : half);
+            nh_ = base + 2 * nblk;
         }
-        if (i + 1 < rounds)  // m >= 2 here, since rounds <= num_vars
-            rc = sc_fold_sums(cf, ext, ch, m, r + 2 * i, nf_, nh_, partial + 6ull * kScMaxBlocks * (i + 1),
-                              &counts.n[i + 1], s);
-        else
-            rc = sc_fold(cf, ext, ch, m, r + 2 * i, nf_, nh_, s);
-        if (rc) return rc;
+        ScChallenges c{};
+        for (uint32_t j = 0; j < K; j++) {
+            c.r[2 * j] = gl_canon(r[2 * (i + j)]);
+            c.r[2 * j + 1] = gl_canon(r[2 * (i + j) + 1]);
+        }
+        const uint32_t blocks = sc_blocks(nblk);
+        for (uint32_t j = 0; j < K; j++) counts.n[i + j] = blocks;
+        uint64_t* part = partial + 6ull * kScMaxBlocks * i;
+        ProfMark pm = prof_begin("sumcheck_pass", s);
+        switch (K * 2 + (ext ? 1 : 0)) {
+            case 2: sc_multi_kernel<false, 1><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            case 3: sc_multi_kernel<true, 1><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            case 4: sc_multi_kernel<false, 2><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            case 5: sc_multi_kernel<true, 2><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            case 6: sc_multi_kernel<false, 3><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            case 7: sc_multi_kernel<true, 3><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            case 8: sc_multi_kernel<false, 4><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+            default: sc_multi_kernel<true, 4><<<blocks, kScThreads, 0, s>>>(cf, ch, nblk, c, nf_, nh_, part); break;
+        }
+        prof_end(pm, s);
+        ZK_LAUNCHED();
         cf = nf_;
         ch = nh_;
         ext = true;
+        i += K;
     }
     ProfMark pm = prof_begin("sumcheck_finish", s);
     sc_finish_kernel<<<rounds, kFinThreads, 0, s>>>(partial, counts, d_y);
