@@ -270,6 +270,9 @@ int emu_lde_rows(const uint64_t* in, uint64_t h, uint64_t in_rows, uint64_t w, u
     return 0;
 }
 
+// The source word of output word t of the Prefix-order transpose.
+uint64_t emu_prefix_source(uint64_t t, uint32_t lrows, uint32_t k, uint32_t E) { return prefix_source(t, lrows, k, E); }
+
 int emu_lde(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup, uint64_t* out,
             uint32_t threads)
 {

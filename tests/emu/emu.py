@@ -58,6 +58,8 @@ def load():
         L.emu_lde.restype = ctypes.c_int
         L.emu_lde_rows.argtypes = [_u64p, _u64, _u64, _u64, ctypes.c_uint32, _u64p, ctypes.c_uint32]
         L.emu_lde_rows.restype = ctypes.c_int
+        L.emu_prefix_source.argtypes = [_u64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        L.emu_prefix_source.restype = _u64
         L.emu_lde_leaf.argtypes = [_u64p, _u64, _u64, ctypes.c_uint32, _u64p, _u64p, _u64p, _u64p, _u64p,
                                    _u64, ctypes.c_int]
         L.emu_lde_leaf.restype = ctypes.c_int

@@ -158,6 +158,24 @@ def test_lde_passes_ragged_rows(emu, oracle, lg, w, lb, rows):
     assert (out == oracle.lde_batch(full, lb)).all()
 
 
+@pytest.mark.parametrize("n_vars,k,E", [(31, 4, 2), (32, 4, 2), (32, 1, 1), (31, 31, 2), (20, 3, 2)])
+def test_prefix_transpose_index_at_full_size(emu, n_vars, k, E):
+    """The Prefix-order transpose's index map (output word t reads word
+    ((j 2^lrows + i) E + c) with t = (i 2^k + j) E + c) in 64 bits, at the
+    largest tables (2^33 words for 32 EF variables), against Python integers
+    on the first, last and scattered words; the map is a permutation of the
+    words (source words distinct and in range on a dense sample)."""
+    lrows = n_vars - k
+    total = E << n_vars
+    ts = [0, 1, E, total - 1, total - E, total // 2, total // 3] + [(total * q) // 97 for q in range(97)]
+    for t in ts:
+        c, e = t % E, t // E
+        j, i = e % (1 << k), e >> k
+        assert emu.emu_prefix_source(t, lrows, k, E) == ((j << lrows) + i) * E + c
+    dense = [emu.emu_prefix_source(t, lrows, k, E) for t in range(total - 4096, total)]
+    assert len(set(dense)) == len(dense) and max(dense) < total
+
+
 @pytest.mark.parametrize("lg,lb", [(8, 2), (10, 2), (12, 2), (11, 3), (13, 3), (16, 2)])
 def test_lde_last_pass_fused_with_leaf_hash(emu, oracle, lg, lb):
     """The fused last NTT pass + leaf hash of the commitment (last_leaf.hpp),

@@ -344,11 +344,8 @@ __global__ __launch_bounds__(256) void prefix_transpose_kernel(const uint64_t* _
                                                                uint32_t lrows, uint32_t k, uint32_t E)
 {
     for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-         t += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t c = t % E, e = t / E;
-        const uint64_t j = e & ((1ull << k) - 1), i = e >> k;
-        out[t] = in[((j << lrows) | i) * E + c];
-    }
+         t += (uint64_t)gridDim.x * blockDim.x)
+        out[t] = in[prefix_source(t, lrows, k, E)];
 }
 
 // commit_extension's encoding (writer.rs:21-86): the 2^n-entry table as a

@@ -152,6 +152,17 @@ inline bool plan_fits(const Plan& p, uint64_t w)
            (n >> p.sb[0]) * w < (1ull << 32);
 }
 
+// Prefix order (writer.rs:43-71): output word t of the committed matrix
+// (E u64 per entry, rows i < 2^lrows, columns j < 2^k) reads word
+// ((j 2^lrows + i) E + c) of the table; all in 64 bits (up to 2^33 words
+// for a 32-variable EF table).
+__host__ __device__ __forceinline__ uint64_t prefix_source(uint64_t t, uint32_t lrows, uint32_t k, uint32_t E)
+{
+    const uint64_t c = t % E, e = t / E;
+    const uint64_t j = e & ((1ull << k) - 1), i = e >> k;
+    return ((j << lrows) | i) * E + c;
+}
+
 // LDS of a pass: the N1 x V tile, the inter-pass twiddle table (kRoleTable)
 // and the step twiddles, unless the sub-DFT is a single step.
 inline size_t pass_lds_bytes(const PassArgs& a)
