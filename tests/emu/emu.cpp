@@ -120,10 +120,11 @@ void run_last_leaf_s(const PassArgs& a, uint64_t* digests, uint64_t digests_len,
         for (uint32_t tid = 0; tid < T; tid++) last_leaf_rows<S, T>(pass_lane(a, t, tid), tid, lds.data(), keep[tid]);
         for (uint32_t tid = 0; tid < T; tid++) {
             if (d15)
-                last_leaf_hash<S, T, true>(a, t, tid, lds.data(), digests, digests_len, C);
+                last_leaf_hash<S, T, true>(tid, lds.data(), C);
             else
-                last_leaf_hash<S, T, false>(a, t, tid, lds.data(), digests, digests_len, C);
+                last_leaf_hash<S, T, false>(tid, lds.data(), C);
         }
+        for (uint32_t tid = 0; tid < T; tid++) last_leaf_store<S, T>(a, t, tid, lds.data(), digests, digests_len);
     }
 }
 

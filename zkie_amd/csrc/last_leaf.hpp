@@ -13,7 +13,10 @@
 //          LDS, row i at words [17 i, 17 i + 16) (the odd stride puts the
 //          later reads of one element of 64 rows on different banks);
 //   hash:  (after a barrier) each thread hashes whole rows from LDS and
-//          writes their digests, so the codeword is never read back from HBM.
+//          leaves their digests in LDS, so the codeword is never read back
+//          from HBM;
+//   store: (after a barrier) lanes write the digests to layer 0, four lanes
+//          per 64-byte digest.
 #pragma once
 
 #include "ntt_pass.hpp"
@@ -117,17 +120,15 @@ __host__ __device__ __forceinline__ void last_leaf_rows(const PassLane& l, uint3
 }
 
 // Leaf digests of the rows of thread tid (rows tid, tid + T, ...), from the
-// row tile (after a barrier that ends the row tile's writes).
+// row tile (after a barrier that ends the row tile's writes), each written
+// canonical over the first 8 words of its own row in the tile (the row is
+// consumed by then, and no other thread reads it).
 template <int S, uint32_t T, bool D15>
-__host__ __device__ __forceinline__ void last_leaf_hash(const PassArgs& a, const PassTile& t, uint32_t tid,
-                                                        const uint64_t* lds, uint64_t* digests, uint64_t digests_len,
-                                                        const P2Consts& C)
+__host__ __device__ __forceinline__ void last_leaf_hash(uint32_t tid, uint64_t* lds, const P2Consts& C)
 {
-    (void)digests_len;
-    const uint32_t shift = a.L - a.s;
 #pragma unroll 1
     for (uint32_t row = tid; row < (1u << S); row += T) {
-        const uint64_t* rp = lds + row * 17;
+        uint64_t* rp = lds + row * 17;
         uint64_t st[16];
 #pragma unroll
         for (int i = 8; i < 16; i++) st[i] = 0;
@@ -140,14 +141,33 @@ __host__ __device__ __forceinline__ void last_leaf_hash(const PassArgs& a, const
             }
             p2_permute<D15>(st, C);
         }
-        const uint64_t d = (t.nat0 + ((uint64_t)row << shift)) * 8;
-        ZK_BOUND(d + 7, digests_len);
-#if defined(__HIP_DEVICE_COMPILE__)
-        ulonglong2* dst = reinterpret_cast<ulonglong2*>(digests + d);
 #pragma unroll
-        for (int k = 0; k < 4; k++) dst[k] = make_ulonglong2(gl_canon(st[2 * k]), gl_canon(st[2 * k + 1]));
+        for (int i = 0; i < 8; i++) rp[i] = gl_canon(st[i]);
+    }
+}
+
+// The tile's digests from LDS to layer 0 (after a barrier that ends the
+// digest writes): four consecutive lanes write the four 16-byte quarters of
+// one 64-byte digest, so each digest reaches the L2 as one piece (a tile's
+// rows are 2^(L - s) rows apart in natural order, so its digests are too).
+template <int S, uint32_t T>
+__host__ __device__ __forceinline__ void last_leaf_store(const PassArgs& a, const PassTile& t, uint32_t tid,
+                                                         const uint64_t* lds, uint64_t* digests, uint64_t digests_len)
+{
+    (void)digests_len;
+    const uint32_t shift = a.L - a.s;
+#pragma unroll 1
+    for (uint32_t q = tid; q < (4u << S); q += T) {
+        const uint32_t row = q >> 2, k = q & 3;
+        ZK_BOUND(row * 17 + 2 * k + 1, (1u << S) * 17);
+        const uint64_t* rp = lds + row * 17 + 2 * k;
+        const uint64_t d = (t.nat0 + ((uint64_t)row << shift)) * 8 + 2 * k;
+        ZK_BOUND(d + 1, digests_len);
+#if defined(__HIP_DEVICE_COMPILE__)
+        *reinterpret_cast<ulonglong2*>(digests + d) = make_ulonglong2(rp[0], rp[1]);
 #else
-        for (int k = 0; k < 8; k++) digests[d + k] = gl_canon(st[k]);
+        digests[d] = rp[0];
+        digests[d + 1] = rp[1];
 #endif
     }
 }

@@ -228,7 +228,9 @@ __global__ __launch_bounds__(fuse_threads<S>()) __attribute__((amdgpu_waves_per_
     __syncthreads();
     last_leaf_rows<S, T>(l, tid, lds, keep);
     __syncthreads();
-    last_leaf_hash<S, T, D15>(a, t, tid, lds, digests, 0, c_p2);
+    last_leaf_hash<S, T, D15>(tid, lds, c_p2);
+    __syncthreads();
+    last_leaf_store<S, T>(a, t, tid, lds, digests, 0);
 }
 
 // Parents [from, to) of `step` children each; slots [to, pad_to) get the
