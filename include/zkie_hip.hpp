@@ -195,6 +195,50 @@ class HipMerkleTreeMmcs {
         return {std::move(cap), std::move(t)};
     }
 
+    /* Whir::commit_batch (crates/zkie-core/src/pcs/whir.rs:476-525): same-size
+     * tables of evaluations stacked table-major into one zero-padded witness,
+     * viewed as rows of 2^log_width, encoded with blowup 2^log_blowup and
+     * committed. The tree's matrix is the codeword. */
+    std::pair<MerkleCap, MerkleTree> commit_batch(const std::vector<std::vector<F>>& evals_batch, uint32_t log_width,
+                                                  uint32_t log_blowup) const
+    {
+        if (evals_batch.empty()) throw Error(ZKIE_ERR_INVALID, "commit_batch: batch must not be empty");
+        const size_t len = evals_batch[0].size();
+        uint32_t arity = 0;
+        while ((size_t(1) << arity) < len) arity++;
+        for (const auto& e : evals_batch)
+            if (e.size() != len || (size_t(1) << arity) != len)
+                throw Error(ZKIE_ERR_INVALID, "commit_batch: all tables must hold the same power-of-two count");
+        const size_t total = evals_batch.size() * len;
+        uint32_t vars = 0;
+        while ((size_t(1) << vars) < total) vars++;
+        if (vars < log_width) throw Error(ZKIE_ERR_INVALID, "commit_batch: the stacked witness fills no row");
+        std::vector<DeviceBuffer> tables;
+        std::vector<const uint64_t*> ptrs;
+        for (const auto& e : evals_batch) {
+            tables.push_back(DeviceBuffer::upload(e));
+            ptrs.push_back(tables.back().data());
+        }
+        MerkleTree t;
+        t.width = size_t(1) << log_width;
+        t.height = (size_t(1) << (vars - log_width)) << log_blowup;
+        uint32_t nl = 0;
+        std::vector<uint64_t> lens(65);
+        check(zkie_merkle_layout(t.height, &nl, lens.data()), "zkie_merkle_layout");
+        lens.resize(nl);
+        size_t digests = 0;
+        for (uint64_t l : lens) digests += l;
+        t.layer_lens = lens;
+        DeviceBuffer stack(size_t(1) << vars);
+        t.mat = DeviceBuffer(t.height * t.width);
+        t.layers = DeviceBuffer(digests * 8);
+        check(zkie_commit_batch(ptrs.data(), (uint32_t)ptrs.size(), arity, log_width, log_blowup, stack.data(),
+                                t.mat.data(), t.layers.data(), t.root.data(), nullptr),
+              "zkie_commit_batch");
+        MerkleCap cap{t.root};
+        return {std::move(cap), std::move(t)};
+    }
+
     /* mmcs/batch.rs:75-121. */
     BatchOpening open_batch(size_t index, const MerkleTree& t) const
     {

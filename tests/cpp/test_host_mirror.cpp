@@ -100,6 +100,37 @@ int main()
         same = same && rows[i][0] == std::vector<F>(cw.row(q[i]), cw.row(q[i]) + 16);
     EXPECT(same, "open_multi_batch rows and pruned proof equal the oracle");
 
+    // commit_batch: three tables of 2^9, stacked table-major into 2^11 (one
+    // zero table of padding), rows of 16, blowup 4
+    {
+        std::vector<std::vector<F>> tabs;
+        std::vector<F> stacked(size_t(1) << 11, 0);
+        for (int i = 0; i < 3; i++) {
+            tabs.push_back(random_matrix(40 + i, 1 << 9, 1).values);
+            std::memcpy(stacked.data() + (size_t(i) << 9), tabs.back().data(), (size_t(1) << 9) * sizeof(F));
+        }
+        auto [bcap, btree] = mmcs.commit_batch(tabs, 4, 2);
+        std::vector<F> bcw((size_t(1) << 9) * 16);
+        or_lde_batch(stacked.data(), 1 << 7, 16, 2, 1, bcw.data());
+        std::vector<uint64_t> blens(65);
+        const uint32_t bnl = or_merkle_num_layers(1 << 9);
+        or_merkle_layer_lens(1 << 9, blens.data());
+        size_t btotal = 0;
+        for (uint32_t i = 0; i < bnl; i++) btotal += blens[i];
+        std::vector<uint64_t> blayers(btotal * 8);
+        zkie::Digest broot{};
+        or_merkle_commit(bcw.data(), 1 << 9, 16, blayers.data(), broot.data());
+        EXPECT(btree.height == (1u << 9) && btree.mat.download() == bcw, "commit_batch codeword equals the oracle");
+        EXPECT(bcap.size() == 1 && bcap[0] == broot, "commit_batch root equals the oracle");
+        bool threw = false;
+        try {
+            mmcs.commit_batch({std::vector<F>(8), std::vector<F>(4)}, 1, 1);
+        } catch (const zkie::Error&) {
+            threw = true;
+        }
+        EXPECT(threw, "commit_batch refuses tables of different sizes");
+    }
+
     // fold of the committed codeword
     std::vector<zkie::Ef> r(4);
     for (int b = 0; b < 4; b++) r[b] = {F(1000 + b), F(7 * b + 1)};
