@@ -67,3 +67,5 @@ def test_refusals(native):
     assert call([0], 1, 4, 2, 1) != 0                           # null table
     assert call([s.addr + 8, a.addr], 2, 4, 2, 1) != 0          # overlaps the stack, not its slot
     assert call([a.addr], 1, 41, 2, 1) != 0                     # arity beyond the limit
+    big = [a.addr] * 512
+    assert call(big, 512, 40, 16, 0) != 0                       # 2^9 x 2^40 entries: beyond 2^48

@@ -111,7 +111,8 @@ def test_eq_table_matches_oracle(native, oracle, t):
 
 @pytest.mark.parametrize("n,m,q,acc", [(0, 1, 0, False), (3, 1, 2, False), (7, 0, 3, True), (8, 2, 5, True),
                                        (9, 2, 0, False), (12, 2, 100, False), (16, 5, 30, True),
-                                       (18, 2, 128, True), (11, 0, 0, False), (11, 0, 0, True)])
+                                       (18, 2, 128, True), (11, 0, 0, False), (11, 0, 0, True), (0, 150, 60, False),
+                                       (0, 40, 200, True), (2, 60, 10, False)])
 def test_constraint_weights_match_oracle(native, oracle, n, m, q, acc):
     """zkie_constraint_weights (the batched constraint of a WHIR round) equals
     the oracle bit for bit: tables split at 8 or more low bits, several

@@ -717,6 +717,9 @@ int zkie_commit_batch(const uint64_t* const* d_tables, uint32_t count, uint32_t 
 {
     if (!d_tables || count == 0 || arity > 40 || log_width > 16 || !d_stack || !d_codeword || !d_layers)
         return ZKIE_ERR_INVALID;
+    // at most 2^48 stacked entries (a codeword row count of at most 2^32
+    // with rows of at most 2^16), so every size below fits in 64 bits
+    if ((uint64_t)count > (1ull << (48 - arity))) return ZKIE_ERR_INVALID;
     const uint64_t len = 1ull << arity;
     const uint64_t total = (uint64_t)count << arity;
     uint32_t vars = 0;  // total_num_vars: the stacked witness has 2^vars entries

@@ -508,9 +508,12 @@ int constraint_weights(const uint64_t* eq_points, uint32_t m, const uint64_t* se
         a.g0[1] = gl_canon(g.c1);
         a.n = n;
         a.h = h;
-        // eq points first, then selection points, as many as fit
+        // eq points first, then selection points, as many as fit: at most
+        // kCwMaxValues values (the argument block) and kCwMaxValues
+        // constraints (the small-table workspace; 0-variable eq points take
+        // no values)
         uint32_t used = 0;
-        while (c < m && used + n <= kCwMaxValues) {
+        while (c < m && used + n <= kCwMaxValues && a.m < kCwMaxValues) {
             for (uint32_t b = 0; b < n; b++) {
                 a.v[2 * (used + b)] = gl_canon(eq_points[2 * ((uint64_t)c * n + b)]);
                 a.v[2 * (used + b) + 1] = gl_canon(eq_points[2 * ((uint64_t)c * n + b) + 1]);
@@ -520,7 +523,7 @@ int constraint_weights(const uint64_t* eq_points, uint32_t m, const uint64_t* se
             c++;
         }
         if (c >= m) {
-            while (c < total && used < kCwMaxValues) {
+            while (c < total && used < kCwMaxValues && a.m + a.q < kCwMaxValues) {
                 a.v[2 * used] = gl_canon(sel[2 * (c - m)]);
                 a.v[2 * used + 1] = gl_canon(sel[2 * (c - m) + 1]);
                 used++;
