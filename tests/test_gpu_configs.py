@@ -142,6 +142,20 @@ def test_workload_full_size_properties(native, oracle, number):
     property_checks(native, oracle, wl, data, out, np.random.default_rng(number))
 
 
+def test_largest_fused_commit_properties(native, oracle):
+    """Configuration 3's pipeline at twice its rows (2^25 x 16, codeword
+    2^27 x 16 = 16 GiB): the transform splits into three 9-bit passes, so the
+    last one is fused with the leaf hash in 512-thread workgroups (one per
+    2^9-row tile, 2^18 of them), checked through the same size-independent
+    properties."""
+    wl = C.CONFIGS[3].scaled(1 << 25)
+    _case("full-size properties", wl.name)
+    data = PL.workload_inputs(wl)
+    d_in = DeviceBuffer.from_array(data)
+    out = PL.run_workload(wl, d_in, with_openings=False)
+    property_checks(native, oracle, wl, data, out, np.random.default_rng(25))
+
+
 @pytest.mark.gpu
 def test_whir_rounds_ood_and_stir_full_size(native, oracle):
     """The WHIR-shaped workload at full size: every round's sumcheck weights
