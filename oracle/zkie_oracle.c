@@ -151,9 +151,32 @@ void or_idft_batch(uint64_t *mat, uint32_t lg_h, uint64_t w)
 /* Horner evaluation of column c of an h x w coefficient matrix at x. */
 uint64_t or_poly_eval(const uint64_t *mat, uint64_t h, uint64_t w, uint64_t c, uint64_t x)
 {
-    uint64_t acc = 0;
-    for (uint64_t j = h; j-- > 0;) acc = or_add(or_mul(acc, x), mat[j * w + c]);
-    return acc;
+    /* Horner over chunks of 2^20 coefficients in parallel: chunk b holds
+     * coefficients [b B, (b + 1) B) and contributes x^(b B) times its own
+     * Horner value. */
+    const uint64_t B = (uint64_t)1 << 20;
+    if (h <= B) {
+        uint64_t acc = 0;
+        for (uint64_t j = h; j-- > 0;) acc = or_add(or_mul(acc, x), mat[j * w + c]);
+        return acc;
+    }
+    const uint64_t nb = (h + B - 1) / B;
+    const uint64_t xB = or_pow(x, B);
+    uint64_t total = 0;
+#pragma omp parallel
+    {
+        uint64_t part = 0;
+#pragma omp for schedule(static)
+        for (int64_t b = 0; b < (int64_t)nb; b++) {
+            const uint64_t lo = (uint64_t)b * B, hi = lo + B < h ? lo + B : h;
+            uint64_t acc = 0;
+            for (uint64_t j = hi; j-- > lo;) acc = or_add(or_mul(acc, x), mat[j * w + c]);
+            part = or_add(part, or_mul(acc, or_pow(xB, (uint64_t)b)));
+        }
+#pragma omp critical
+        total = or_add(total, part);
+    }
+    return total;
 }
 
 /* Polynomial checksum sum_i v[i] z^i (Horner), a fingerprint of a vector. */

@@ -228,3 +228,28 @@ def test_lde_commit(native, oracle, h, w, lb, shift):
     for a, b in zip(got, layers):
         assert (a == b).all()
     assert (tree.root == root).all()
+
+
+def test_lde_at_the_largest_transform(native, oracle):
+    """zkie_lde_batch at the library's largest transform: 2^30 coefficients of
+    one column, blowup 4, a codeword of 2^32 rows (32 GiB; the reference caps
+    its GPU DFT at 2^18 rows, dft_cuda.rs:96). Sampled rows equal direct
+    evaluation at w_{2^32}^t (Horner over the 2^30 coefficients), and the
+    inverse DFT of the whole codeword returns the zero-padded input."""
+    _case("lde 2^30 -> 2^32 rows")
+    h, lb = 1 << 30, 2
+    n = h << lb
+    x = native.gen_inputs(77, h, 0)
+    d_in = DeviceBuffer.from_array(x)
+    d_cw = DeviceBuffer(n)
+    check(native.load().zkie_lde_batch(d_in.addr, h, 1, lb, 1, d_cw.addr, None), "zkie_lde_batch")
+    del d_in
+    g = oracle.two_adic_generator(32)
+    col = x.reshape(h, 1)
+    rng = np.random.default_rng(32)
+    for t in [0, 1, n // 4, n // 2, n - 1] + [int(v) for v in rng.integers(0, n, 3)]:
+        assert int(d_cw.download(1, t)[0]) == oracle.poly_eval(col, 0, pow(g, t, P)), t
+    check(native.load().zkie_idft_batch(d_cw.addr, 32, 1, None), "zkie_idft_batch")
+    back = d_cw.download()
+    assert (back[:h] == x).all()
+    assert not back[h:].any()

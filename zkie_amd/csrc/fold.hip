@@ -39,14 +39,15 @@ __global__ __launch_bounds__(256) void fold_kernel(const uint64_t* __restrict__ 
     if constexpr (RW == 8 || RW == 16) {
         // rows of 64 or 128 bytes: staged through LDS so HBM serves each once
         __shared__ uint64_t tile[256 * (RW + 1)];
-        const uint64_t first = (uint64_t)blockIdx.x * 256;
+        const uint64_t first = flat_block() * 256;
+        if (first >= h) return;  // the last row of a two-dimensional grid
         const uint32_t nrows = h - first < 256 ? (uint32_t)(h - first) : 256u;
         stage_rows<RW>(mat, first, nrows, tile);
         if (threadIdx.x >= nrows) return;
         t = first + threadIdx.x;
         row = tile + threadIdx.x * (RW + 1);
     } else {
-        t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        t = flat_block() * blockDim.x + threadIdx.x;
         if (t >= h) return;
         row = mat + t * RW;
     }
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void fold_kernel_rt(const uint64_t* __restrict
                                                       uint32_t k, const uint64_t* __restrict__ eq,
                                                       uint64_t* __restrict__ out)
 {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t t = flat_block() * blockDim.x + threadIdx.x;
     if (t >= h) return;
     const uint64_t Wd = 1ull << k;
     uint64_t s0 = 0, s1 = 0;
@@ -126,7 +127,7 @@ int fold_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ext, const
     if (((uintptr_t)d_mat | (uintptr_t)d_out) & 15) return ZKIE_ERR_INVALID;
     if (h == 0) return ZKIE_OK;
     const std::vector<uint64_t> eq = eq_table(r, k);
-    const unsigned grid = (unsigned)((h + 255) / 256);
+    const dim3 grid = grid_of((h + 255) / 256, 256);
     if (k <= 6) {
         EqArg ea{};
         for (size_t j = 0; 2 * j < eq.size(); j++) {
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const uint64_t* __rest
                                                           const uint64_t* __restrict__ ids, uint64_t n,
                                                           uint64_t* __restrict__ dst)
 {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t t = flat_block() * blockDim.x + threadIdx.x;
     if (t >= n * width) return;
     const uint64_t k = t / width, e = t % width;
     dst[t] = src[ids[k] * width + e];
@@ -243,7 +244,7 @@ int fold_rows_at_device(const uint64_t* d_mat, uint64_t h, uint32_t k, int is_ex
     uint64_t* d_rows = buf + ids_words;
     uint64_t* d_out = d_rows + rows_words;
     ZK_TRY(hipMemcpyAsync(d_ids, ids, n * 8, hipMemcpyHostToDevice, s));
-    gather_rows_kernel<<<(unsigned)((n * width + 255) / 256), 256, 0, s>>>(d_mat, width, d_ids, n, d_rows);
+    gather_rows_kernel<<<grid_of((n * width + 255) / 256, 256), 256, 0, s>>>(d_mat, width, d_ids, n, d_rows);
     ZK_LAUNCHED();
     const int rc = fold_device(d_rows, n, k, is_ext, r, d_out, s);
     if (rc) return rc;

@@ -178,7 +178,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
     uint64_t st[16];
     if constexpr (W == 8 || W == 16) {
         __shared__ uint64_t tile[256 * (W + 1)];
-        const uint64_t first = row0 + (uint64_t)blockIdx.x * 256;
+        const uint64_t first = row0 + flat_block() * 256;
+        if (first >= row_end) return;  // the last row of a two-dimensional grid
         const uint32_t nrows = row_end - first < 256 ? (uint32_t)(row_end - first) : 256u;
         stage_rows<W>(mat, first, nrows, tile);
         if (threadIdx.x >= nrows) return;
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
         }
         store_digest(digests + (first + threadIdx.x) * 8, st);
     } else {
-        const uint64_t row = row0 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        const uint64_t row = row0 + flat_block() * blockDim.x + threadIdx.x;
         if (row >= row_end) return;
         hash_row<W, D15>(mat + row * (W > 0 ? (uint64_t)W : w), w, st);
         store_digest(digests + row * 8, st);
@@ -212,7 +213,8 @@ __global__ __launch_bounds__(fuse_threads<S>()) __attribute__((amdgpu_waves_per_
     constexpr uint32_t T = fuse_threads<S>();
     const uint32_t tid = threadIdx.x;
     __builtin_assume(tid < T);
-    const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
+    const uint64_t bid = flat_block();
+    if (bid >= pass_blocks(a)) return;  // the last row of a two-dimensional grid
     const PassTile t = pass_tile(a, bid);
     const PassLane l = pass_lane(a, t, tid);
     pass_tables<S, kRoleLast>(a, t, tid, T, lds);
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
                                                        uint64_t* __restrict__ next, uint64_t from,
                                                        uint64_t to, uint64_t pad_to, uint32_t step)
 {
-    const uint64_t i = from + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = from + flat_block() * blockDim.x + threadIdx.x;
     if (i >= pad_to) return;
     uint64_t st[16];
     if (i >= to) {
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) void compress_x16_kernel(const uint64_t* __res
                                                            uint64_t* __restrict__ next, uint64_t from,
                                                            uint64_t to, uint64_t pad_to, uint32_t step)
 {
-    const uint64_t p = from + ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / 16;
+    const uint64_t p = from + (flat_block() * blockDim.x + threadIdx.x) / 16;
     const uint32_t i = threadIdx.x & 15;
     if (p >= pad_to) return;
     if (p >= to) {
@@ -330,13 +332,13 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint64_t* __restrict_
                                                      const uint64_t* __restrict__ ids,
                                                      uint64_t count, uint64_t* __restrict__ dst)
 {
-    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t t = flat_block() * blockDim.x + threadIdx.x;
     if (t >= count * len) return;
     const uint64_t k = t / len, e = t % len;
     dst[t] = src[ids[k] * stride + e];
 }
 
-unsigned grid_for(uint64_t n, unsigned block = 256) { return (unsigned)((n + block - 1) / block); }
+dim3 grid_for(uint64_t n, unsigned block = 256) { return grid_of((n + block - 1) / block, block); }
 
 // Launch the leaf kernel for rows [r0, r1) with a width specialisation.
 int launch_leaves(const uint64_t* mat, uint64_t* dig, uint64_t r0, uint64_t r1, uint64_t w,
@@ -345,7 +347,7 @@ int launch_leaves(const uint64_t* mat, uint64_t* dig, uint64_t r0, uint64_t r1, 
     if (r1 <= r0) return ZKIE_OK;
     // Even-width rows are read with 16-byte loads; digests are stored as 16-byte pairs.
     if (((uintptr_t)dig & 15) || ((w % 2) == 0 && ((uintptr_t)mat & 15))) return ZKIE_ERR_INVALID;
-    const unsigned grid = grid_for(r1 - r0);
+    const dim3 grid = grid_for(r1 - r0);
     ProfMark m = prof_begin("p2_leaf", s);
 #define ZK_LEAF(WW)                                                                                   \
     do {                                                                                              \
@@ -471,15 +473,7 @@ hipError_t launch_last_leaf_s(const PassArgs& a, uint64_t* digests, hipStream_t 
             raised[dev] = shmem;
         }
     }
-    const uint64_t blocks = pass_blocks(a);
-    dim3 grid;
-    if (blocks <= 0x7FFFFFFFull) {
-        grid = dim3((unsigned)blocks, 1, 1);
-    } else {
-        if ((blocks % 65536) != 0) return hipErrorInvalidValue;
-        grid = dim3(65536u, (unsigned)(blocks / 65536), 1);
-    }
-    ntt_last_leaf_kernel<S, D15><<<grid, fuse_threads<S>(), shmem, s>>>(a, digests);
+    ntt_last_leaf_kernel<S, D15><<<grid_of(pass_blocks(a), fuse_threads<S>()), fuse_threads<S>(), shmem, s>>>(a, digests);
     return hipGetLastError();
 }
 

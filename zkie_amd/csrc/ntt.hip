@@ -60,7 +60,8 @@ __global__ __launch_bounds__(kNttThreads) void ntt_pass_kernel(PassArgs a)
     const uint32_t tid = threadIdx.x;
     __builtin_assume(tid < T);  // lets the step loops drop their item-count checks
     constexpr int n = pass_steps<S>();
-    const uint64_t bid = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
+    const uint64_t bid = flat_block();
+    if (bid >= pass_blocks(a)) return;  // the last row of a two-dimensional grid
     const PassTile t = pass_tile(a, bid);
     const PassLane l = pass_lane(a, t, tid);
     if constexpr (n == 1) {
@@ -116,15 +117,7 @@ hipError_t launch_one(const PassArgs& a, uint64_t blocks, size_t shmem, hipStrea
             raised[dev] = shmem;
         }
     }
-    dim3 grid;
-    if (blocks <= 0x7FFFFFFFull) {
-        grid = dim3((unsigned)blocks, 1, 1);
-    } else {
-        const uint64_t gx = 65536;
-        if ((blocks % gx) != 0) return hipErrorInvalidValue;
-        grid = dim3((unsigned)gx, (unsigned)(blocks / gx), 1);
-    }
-    ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV, ROWS><<<grid, kNttThreads, shmem, s>>>(a);
+    ntt_pass_kernel<S, KNZ, INV, ROLE, LOGV, ROWS><<<grid_of(blocks, kNttThreads), kNttThreads, shmem, s>>>(a);
     return hipGetLastError();
 }
 

@@ -24,6 +24,19 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
         if (zk_e_ != hipSuccess) return (int)zk_e_;    \
     } while (0)
 
+// A grid of at least `blocks` workgroups of `threads` work-items. A dispatch
+// holds its size in work-items as a 32-bit number per dimension, so past
+// 2^32 work-items the grid becomes rows of 2^16 workgroups; the last row can
+// overshoot, so kernels launched this way check their index against their
+// size, and read their workgroup index with flat_block().
+inline dim3 grid_of(uint64_t blocks, uint32_t threads)
+{
+    if (blocks * threads < (1ull << 32)) return dim3((unsigned)blocks, 1, 1);
+    return dim3(65536u, (unsigned)((blocks + 65535) / 65536), 1);
+}
+
+__device__ __forceinline__ uint64_t flat_block() { return blockIdx.x + (uint64_t)blockIdx.y * gridDim.x; }
+
 // Grow-only device scratch, one buffer per (device, slot); the same role as
 // the reference's CudaBuffer arenas (cuda_buffer.rs:7-57), which the
 // reference serialises behind a Mutex (cuda_buffer.rs:59).

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(kScThreads) void sc_fold_kernel(const uint64_t* __r
                                                              uint64_t* __restrict__ f_out,
                                                              uint64_t* __restrict__ h_out)
 {
-    const uint64_t s = (uint64_t)blockIdx.x * kScThreads + threadIdx.x;
+    const uint64_t s = flat_block() * kScThreads + threadIdx.x;
     if (s >= half) return;
     const Ef r{r0, r1};
     const Ef f0 = sc_load_f<FEXT>(f, 2 * s), f1 = sc_load_f<FEXT>(f, 2 * s + 1);
@@ -363,9 +363,9 @@ int sc_fold(const uint64_t* d_f, bool f_ext, const uint64_t* d_h, uint32_t m, co
     const uint64_t r0 = gl_canon(r[0]), r1 = gl_canon(r[1]);
     ProfMark pm = prof_begin("sumcheck_fold", s);
     if (f_ext)
-        sc_fold_kernel<true><<<(unsigned)blocks, kScThreads, 0, s>>>(d_f, d_h, half, r0, r1, d_f_out, d_h_out);
+        sc_fold_kernel<true><<<grid_of(blocks, kScThreads), kScThreads, 0, s>>>(d_f, d_h, half, r0, r1, d_f_out, d_h_out);
     else
-        sc_fold_kernel<false><<<(unsigned)blocks, kScThreads, 0, s>>>(d_f, d_h, half, r0, r1, d_f_out, d_h_out);
+        sc_fold_kernel<false><<<grid_of(blocks, kScThreads), kScThreads, 0, s>>>(d_f, d_h, half, r0, r1, d_f_out, d_h_out);
     prof_end(pm, s);
     ZK_LAUNCHED();
     return ZKIE_OK;
