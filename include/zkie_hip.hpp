@@ -15,7 +15,9 @@
  *                               weight table, EF rounds;
  *   zkie::serialize_batch_prover_data_into, zkie::restore_batch_prover_data_from
  *                            <- the prover-data part of the batch cache
- *                               (crates/zkie-core/src/pcs/whir.rs:542-602).
+ *                               (crates/zkie-core/src/pcs/whir.rs:542-602);
+ *   zkie::write_header, zkie::read_header
+ *                            <- the batch cache header (pcs/cache.rs:7-70).
  * Matrices are p3's RowMajorMatrix<F> (values row-major, canonical u64).
  * Errors: every non-zero status of the C ABI throws zkie::Error carrying it;
  * there is no CPU fallback here (the reference's Rust caller keeps its own,
@@ -313,6 +315,133 @@ inline MerkleTree restore_batch_prover_data_from(std::istream& is, size_t h, siz
     check(zkie_prover_data_read(read, &is, h, w, t.mat.data(), t.layers.data(), t.root.data(), nullptr),
           "zkie_prover_data_read");
     return t;
+}
+
+/* The batch cache header (crates/zkie-core/src/pcs/cache.rs:7-70):
+ * write_header stores (BATCH_CACHE_MAGIC, BatchCacheMetadata, Commitment) the
+ * way bincode 1.3.3's serialize_into encodes that tuple (Cargo.lock pins
+ * bincode 1.3.3): integers fixed-width little-endian, strings and sequences
+ * preceded by their length as a u64, fixed-size arrays, tuples and structs
+ * field by field in declaration order, nothing else. The commitment is
+ * p3's MerkleCap<F, [F; 8]>, a sequence of digests (cap height 0: one), each
+ * field element a u64. The prover data (serialize_batch_prover_data_into)
+ * follows the header in the cache file (whir.rs:887-889). */
+constexpr uint32_t kBatchCacheSchemaVersion = 2;  // cache.rs:7
+constexpr char kBatchCacheMagic[8] = {'Z', 'K', 'I', 'E', 'B', 'C', 'H', '2'};
+
+/* BatchCacheMetadata (cache.rs:10-22). */
+struct BatchCacheMetadata {
+    uint32_t schema_version = kBatchCacheSchemaVersion;
+    std::string model_id;
+    std::string group_id;
+    std::vector<std::string> table_ids;  // ordered model tensors: position = committed table index
+    uint32_t table_arity = 0;
+    uint32_t num_tables = 0;
+    uint32_t security_level = 0;
+    uint32_t pow_bits = 0;
+    std::array<uint8_t, 32> source_digest{};
+
+    bool operator==(const BatchCacheMetadata& o) const
+    {
+        return schema_version == o.schema_version && model_id == o.model_id && group_id == o.group_id &&
+               table_ids == o.table_ids && table_arity == o.table_arity && num_tables == o.num_tables &&
+               security_level == o.security_level && pow_bits == o.pow_bits && source_digest == o.source_digest;
+    }
+};
+
+namespace detail {
+inline void put_u32(std::ostream& os, uint32_t v)
+{
+    char b[4];
+    for (int i = 0; i < 4; i++) b[i] = static_cast<char>((v >> (8 * i)) & 0xFF);
+    os.write(b, 4);
+}
+inline void put_u64(std::ostream& os, uint64_t v)
+{
+    char b[8];
+    for (int i = 0; i < 8; i++) b[i] = static_cast<char>((v >> (8 * i)) & 0xFF);
+    os.write(b, 8);
+}
+inline void put_str(std::ostream& os, const std::string& s)
+{
+    put_u64(os, s.size());
+    os.write(s.data(), static_cast<std::streamsize>(s.size()));
+}
+inline void get_bytes(std::istream& is, char* dst, size_t n)
+{
+    is.read(dst, static_cast<std::streamsize>(n));
+    if (is.gcount() != static_cast<std::streamsize>(n)) throw Error(ZKIE_ERR_IO, "read_header: short stream");
+}
+inline uint64_t get_uint(std::istream& is, int bytes)
+{
+    unsigned char b[8] = {0};
+    get_bytes(is, reinterpret_cast<char*>(b), static_cast<size_t>(bytes));
+    uint64_t v = 0;
+    for (int i = bytes; i-- > 0;) v = (v << 8) | b[i];
+    return v;
+}
+// Lengths beyond this are refused instead of allocated (a corrupt header).
+constexpr uint64_t kMaxHeaderLen = uint64_t(1) << 24;
+inline uint64_t get_len(std::istream& is)
+{
+    const uint64_t n = get_uint(is, 8);
+    if (n > kMaxHeaderLen) throw Error(ZKIE_ERR_INVALID, "read_header: length out of range");
+    return n;
+}
+inline std::string get_str(std::istream& is)
+{
+    std::string s(get_len(is), '\0');
+    if (!s.empty()) get_bytes(is, &s[0], s.size());
+    return s;
+}
+}  // namespace detail
+
+/* cache::write_header (cache.rs:51-58). The metadata's table count must
+ * match its table identifiers (BatchCacheMetadata::new, cache.rs:36). */
+inline void write_header(std::ostream& os, const BatchCacheMetadata& m, const MerkleCap& commitment)
+{
+    if (m.schema_version != kBatchCacheSchemaVersion || m.table_ids.size() != m.num_tables)
+        throw Error(ZKIE_ERR_INVALID, "write_header: metadata");
+    os.write(kBatchCacheMagic, 8);
+    detail::put_u32(os, m.schema_version);
+    detail::put_str(os, m.model_id);
+    detail::put_str(os, m.group_id);
+    detail::put_u64(os, m.table_ids.size());
+    for (const auto& id : m.table_ids) detail::put_str(os, id);
+    detail::put_u32(os, m.table_arity);
+    detail::put_u32(os, m.num_tables);
+    detail::put_u32(os, m.security_level);
+    detail::put_u32(os, m.pow_bits);
+    os.write(reinterpret_cast<const char*>(m.source_digest.data()), 32);
+    detail::put_u64(os, commitment.size());
+    for (const auto& d : commitment)
+        for (F x : d) detail::put_u64(os, x);
+    if (!os.good()) throw Error(ZKIE_ERR_IO, "write_header");
+}
+
+/* cache::read_header (cache.rs:60-70): refuses another magic or schema
+ * version, as the reference does. */
+inline std::pair<BatchCacheMetadata, MerkleCap> read_header(std::istream& is)
+{
+    char magic[8];
+    detail::get_bytes(is, magic, 8);
+    BatchCacheMetadata m;
+    m.schema_version = static_cast<uint32_t>(detail::get_uint(is, 4));
+    if (std::string(magic, 8) != std::string(kBatchCacheMagic, 8) || m.schema_version != kBatchCacheSchemaVersion)
+        throw Error(ZKIE_ERR_INVALID, "read_header: unsupported batch cache format");
+    m.model_id = detail::get_str(is);
+    m.group_id = detail::get_str(is);
+    const uint64_t n = detail::get_len(is);
+    for (uint64_t i = 0; i < n; i++) m.table_ids.push_back(detail::get_str(is));
+    m.table_arity = static_cast<uint32_t>(detail::get_uint(is, 4));
+    m.num_tables = static_cast<uint32_t>(detail::get_uint(is, 4));
+    m.security_level = static_cast<uint32_t>(detail::get_uint(is, 4));
+    m.pow_bits = static_cast<uint32_t>(detail::get_uint(is, 4));
+    detail::get_bytes(is, reinterpret_cast<char*>(m.source_digest.data()), 32);
+    MerkleCap cap(detail::get_len(is));
+    for (auto& d : cap)
+        for (F& x : d) x = detail::get_uint(is, 8);
+    return {std::move(m), std::move(cap)};
 }
 
 /* Row fold (prover/mod.rs:257-290; mle.rs:8-22 with variable 0 the least

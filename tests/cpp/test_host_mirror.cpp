@@ -199,6 +199,28 @@ int main()
     }
     EXPECT(threw, "restoring a stream of another shape throws zkie::Error(ZKIE_ERR_INVALID)");
 
+    // the whole batch cache, as the reference's round trip writes it
+    // (whir.rs:866-905): header, then the prover data; read back in order
+    {
+        zkie::BatchCacheMetadata meta;
+        meta.model_id = "test-model";
+        meta.group_id = "group-0";
+        meta.table_ids = {"layer-0-weight"};
+        meta.table_arity = 13;
+        meta.num_tables = 1;
+        meta.security_level = 32;
+        meta.pow_bits = 10;
+        meta.source_digest.fill(7);
+        std::stringstream file;
+        zkie::write_header(file, meta, cap);
+        zkie::serialize_batch_prover_data_into(tree, file);
+        const auto hdr = zkie::read_header(file);
+        const auto again = zkie::restore_batch_prover_data_from(file, h, 16);
+        EXPECT(hdr.first == meta && hdr.second == cap && again.root == tree.root &&
+                   again.mat.download() == tree.mat.download(),
+               "cache file: header then prover data read back in order");
+    }
+
     // error path: an index outside the tree is a status, thrown as zkie::Error
     threw = false;
     try {
