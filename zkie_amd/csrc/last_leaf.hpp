@@ -139,7 +139,7 @@ __host__ __device__ __forceinline__ void last_leaf_hash(uint32_t tid, uint64_t* 
                 ZK_BOUND(row * 17 + 8 * b + i, (1u << S) * 17);
                 st[i] = rp[8 * b + i];
             }
-            p2_permute<D15>(st, C);
+            p2_permute<D15, kOutAbsorb>(st, C, b == 1);
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) rp[i] = gl_canon(st[i]);

@@ -148,13 +148,17 @@ __device__ __forceinline__ void hash_row(const uint64_t* __restrict__ row, uint6
 #pragma unroll
                 for (int i = 0; i < 8; i++) st[i] = row[8 * b + i];
             }
-            p2_permute<D15>(st, c_p2);
+            // a partial last chunk keeps the rate words it does not overwrite
+            if constexpr (kRem == 0)
+                p2_permute<D15, kOutAbsorb>(st, c_p2, b == kFull - 1);
+            else
+                p2_permute<D15>(st, c_p2);
         }
         if (kRem) {
 #pragma unroll
             for (int i = 0; i < 8; i++)
                 if (i < kRem) st[i] = row[8 * kFull + i];
-            p2_permute<D15>(st, c_p2);
+            p2_permute<D15, kOutDigest>(st, c_p2);
         }
     } else {
 #pragma unroll 1
@@ -190,7 +194,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void l
         for (int b = 0; b < W / 8; b++) {
 #pragma unroll
             for (int i = 0; i < 8; i++) st[i] = row[8 * b + i];
-            p2_permute<D15>(st, c_p2);
+            p2_permute<D15, kOutAbsorb>(st, c_p2, b == W / 8 - 1);
         }
         store_digest(digests + (first + threadIdx.x) * 8, st);
     } else {
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 #pragma unroll
         for (int k = 8; k < 16; k++) st[k] = 0;
     }
-    p2_permute<D15>(st, c_p2);
+    p2_permute<D15, kOutDigest>(st, c_p2);
     store_digest(next + i * 8, st);
 }
 

@@ -107,10 +107,15 @@ __host__ __device__ __forceinline__ void mat4_wide(const uint64_t* x, uint64_t* 
 // through the layer as exact 64-bit sums (z below 5 2^32, M4 z below 35 2^32
 // plus a constant's half), and each output is reduced once from its two
 // sums. RC: kRcNone, kRcAll (rc[i] added to word i), kRcLane0 (rc[0] added
-// to word 0 only, the constant of the first internal round).
+// to word 0 only, the constant of the first internal round). GROUPS selects
+// the output groups of four words that are formed (bit g: words 4g..4g+3);
+// the other words are left holding their inputs, for a caller that never
+// reads them (the last layer of a permutation whose caller keeps only the
+// digest, or only the capacity before the next absorb overwrites the rate).
 enum { kRcNone = 0, kRcAll = 1, kRcLane0 = 2 };
+enum { kOutAll = 0xF, kOutDigest = 0x3, kOutCapacity = 0xC };
 
-template <int RC>
+template <int RC, int GROUPS = kOutAll>
 __host__ __device__ __forceinline__ void mds_light16_rc(uint64_t* st, const uint64_t* rc)
 {
     uint64_t sl[4], sh[4];
@@ -125,6 +130,7 @@ __host__ __device__ __forceinline__ void mds_light16_rc(uint64_t* st, const uint
     uint64_t w[16];  // lanes whose output still needs + eps (one shared rare branch)
 #pragma unroll
     for (int j = 0; j < 16; j += 4) {
+        if (!((GROUPS >> (j >> 2)) & 1)) continue;
         uint64_t zl[4], zh[4], yl[4], yh[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -145,10 +151,12 @@ __host__ __device__ __forceinline__ void mds_light16_rc(uint64_t* st, const uint
     }
     uint64_t any = 0;
 #pragma unroll
-    for (int i = 0; i < 16; i++) any |= w[i];
+    for (int i = 0; i < 16; i++)
+        if ((GROUPS >> (i >> 2)) & 1) any |= w[i];
     if (__builtin_expect(any != 0, 0)) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) gl_fold_eps(st[i], w[i]);
+        for (int i = 0; i < 16; i++)
+            if ((GROUPS >> (i >> 2)) & 1) gl_fold_eps(st[i], w[i]);
     }
 }
 
@@ -279,8 +287,15 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
     internal_round_core<DIAG15_IS_INV_2_32>(st, 0, diag15);
 }
 
-template <bool DIAG15_IS_INV_2_32>
-__host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts& C)
+// OUT: the output words the caller reads (kOutAll, kOutDigest for words
+// 0..7, kOutCapacity for words 8..15), or kOutAbsorb: the caller passes
+// last = whether this is the last absorb of a sponge (digest) or not
+// (capacity), a value uniform over the wave. Words outside OUT are left
+// undefined.
+enum { kOutAbsorb = 0 };
+
+template <bool DIAG15_IS_INV_2_32, int OUT = kOutAll>
+__host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts& C, bool last = true)
 {
     // Initial linear layer fused with the first round's constants.
     mds_light16_rc<kRcAll>(st, C.ext[0]);
@@ -299,7 +314,12 @@ __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts
 #pragma unroll
             for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
         } else if (r == 7) {
-            mds_light16_rc<kRcNone>(st, nullptr);
+            if (OUT != kOutAbsorb)
+                mds_light16_rc<kRcNone, OUT>(st, nullptr);
+            else if (last)
+                mds_light16_rc<kRcNone, kOutDigest>(st, nullptr);
+            else
+                mds_light16_rc<kRcNone, kOutCapacity>(st, nullptr);
         } else {
             mds_light16_rc<kRcAll>(st, C.ext[r + 1]);
         }
