@@ -13,7 +13,6 @@
 #include <vector>
 
 #include "gl64.hpp"
-#include "row_stage.hpp"
 #include "runtime.hpp"
 
 namespace zk {
@@ -36,16 +35,21 @@ __global__ __launch_bounds__(256) void fold_kernel(const uint64_t* __restrict__ 
     constexpr int RW = EXT ? 2 * Wd : Wd;  // u64 per row
     const uint64_t* row;
     uint64_t t;
-    if constexpr (RW == 8 || RW == 16) {
-        // rows of 64 or 128 bytes: staged through LDS so HBM serves each once
-        __shared__ uint64_t tile[256 * (RW + 1)];
-        const uint64_t first = flat_block() * 256;
-        if (first >= h) return;  // the last row of a two-dimensional grid
-        const uint32_t nrows = h - first < 256 ? (uint32_t)(h - first) : 256u;
-        stage_rows<RW>(mat, first, nrows, tile);
-        if (threadIdx.x >= nrows) return;
-        t = first + threadIdx.x;
-        row = tile + threadIdx.x * (RW + 1);
+    uint64_t rowv[RW % 2 == 0 && RW <= 16 ? RW : 2];
+    if constexpr (RW % 2 == 0 && RW <= 16) {
+        // rows of at most 128 bytes: each lane issues all of its row's 16-byte
+        // loads at once (the 16-byte pieces of a wave's rows cover whole
+        // lines across the loads, so HBM serves each line once)
+        t = flat_block() * blockDim.x + threadIdx.x;
+        if (t >= h) return;
+        const ulonglong2* src = reinterpret_cast<const ulonglong2*>(mat + t * RW);
+#pragma unroll
+        for (int i = 0; i < RW / 2; i++) {
+            const ulonglong2 v = src[i];
+            rowv[2 * i] = v.x;
+            rowv[2 * i + 1] = v.y;
+        }
+        row = rowv;
     } else {
         t = flat_block() * blockDim.x + threadIdx.x;
         if (t >= h) return;

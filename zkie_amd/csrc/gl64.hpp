@@ -19,6 +19,29 @@
 
 namespace zk {
 
+// Streaming global accesses (codeword passes read and write every word
+// once): loads and stores with the non-temporal hint, plain on the host.
+
+template <class T>
+__host__ __device__ __forceinline__ T ld_nt(const T* p)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+template <class T>
+__host__ __device__ __forceinline__ void st_nt(T* p, T v)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_nontemporal_store(v, p);
+#else
+    *p = v;
+#endif
+}
+
 constexpr uint64_t P = 0xFFFFFFFF00000001ull;
 constexpr uint64_t EPS = 0xFFFFFFFFull;
 constexpr uint64_t HALF = 0x7FFFFFFF80000001ull;  // (p + 1) / 2

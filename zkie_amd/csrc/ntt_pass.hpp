@@ -81,6 +81,16 @@ struct PassTile {
 //   kRoleLastScale  the same, times the pass scale (1/n of an inverse DFT).
 enum PassRole { kRoleTwiddle = 0, kRoleTable = 1, kRoleLast = 2, kRoleLastScale = 3 };
 
+// The first pass of a zero-padded LDE (fewer than 8 non-zero step-0 inputs)
+// reads its input once and writes 8 / KNZ times as much: its HBM loads and
+// stores carry the non-temporal hint (ld_nt, st_nt), which measured faster
+// there and not in the other passes.
+template <int KNZ>
+__host__ __device__ constexpr bool pass_streams()
+{
+    return KNZ < 8;
+}
+
 __host__ __device__ __forceinline__ uint32_t bit_reverse(uint32_t x, uint32_t bits)
 {
     return bits ? (__builtin_bitreverse32(x) >> (32 - bits)) : 0u;
@@ -307,7 +317,7 @@ __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const Pa
                 if (k < KNZ) {
                     const uint64_t idx = gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride;
                     ZK_BOUND(idx, a.in_len);
-                    x[u][k] = a.in[idx];
+                    x[u][k] = pass_streams<KNZ>() ? ld_nt(a.in + idx) : a.in[idx];
                 } else {
                     x[u][k] = 0;
                 }
@@ -333,7 +343,7 @@ __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const Pa
                     const bool in = pos < l.pos_lim;
                     const uint64_t idx = in ? gbase + (uint64_t)((uint32_t)k << QL) * a.in_stride : 0;
                     ZK_BOUND(idx, a.in_len);
-                    const uint64_t val = a.in[idx];
+                    const uint64_t val = pass_streams<KNZ>() ? ld_nt(a.in + idx) : a.in[idx];
                     x[u][k] = in ? val : 0;
                 } else {
                     x[u][k] = 0;
@@ -351,7 +361,8 @@ __host__ __device__ __forceinline__ void step_gather(const PassArgs& a, const Pa
 // w_{2^BS}^(f q) from the LDS table wtab (w_512^k), then the outputs to the
 // LDS tile or, in the last step (TO_GLOBAL), with the pass role's treatment
 // to HBM.
-template <int S, int RL, int BS, bool INV, bool TO_GLOBAL, int ROLE, int LOGV, int NZ = (1 << RL)>
+template <int S, int RL, int BS, bool INV, bool TO_GLOBAL, int ROLE, int LOGV, int NZ = (1 << RL),
+          bool STREAM = false>
 __host__ __device__ __forceinline__ void step_finish(const PassArgs& a, const PassTile& t, const PassLane& l,
                                                      uint32_t it0, uint32_t T, uint64_t* lds,
                                                      const uint64_t* wtab, const uint64_t* twtab,
@@ -420,7 +431,10 @@ __host__ __device__ __forceinline__ void step_finish(const PassArgs& a, const Pa
                 }
                 const uint64_t oidx = obase + (uint64_t)fi * a.out_stride;
                 ZK_BOUND(oidx, a.out_len);
-                a.out[oidx] = val;
+                if (STREAM)
+                    st_nt(a.out + oidx, val);
+                else
+                    a.out[oidx] = val;
             }
         } else {
             const uint32_t lbase = (base << logV) | v;
@@ -436,7 +450,8 @@ __host__ __device__ __forceinline__ void step_finish(const PassArgs& a, const Pa
 }
 
 // One radix-2^RL DIF step: every round of gather + finish.
-template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE, int LOGV>
+template <int S, int RL, int BS, int KNZ, bool INV, bool FROM_GLOBAL, bool TO_GLOBAL, int ROLE, int LOGV,
+          bool STREAM = pass_streams<KNZ>()>
 __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassTile& t, const PassLane& l,
                                                   uint32_t tid, uint32_t T, uint64_t* lds, const uint64_t* wtab,
                                                   const uint64_t* twtab)
@@ -446,7 +461,8 @@ __host__ __device__ __forceinline__ void ntt_step(const PassArgs& a, const PassT
     for (uint32_t it0 = tid; it0 < items; it0 += kStepU * T) {
         uint64_t x[kStepU][1 << RL];
         step_gather<S, RL, BS, KNZ, FROM_GLOBAL, LOGV>(a, t, l, it0, T, lds, x);
-        step_finish<S, RL, BS, INV, TO_GLOBAL, ROLE, LOGV, FROM_GLOBAL ? KNZ : 8>(a, t, l, it0, T, lds, wtab, twtab, x);
+        step_finish<S, RL, BS, INV, TO_GLOBAL, ROLE, LOGV, FROM_GLOBAL ? KNZ : 8, STREAM>(a, t, l, it0, T, lds,
+                                                                                      wtab, twtab, x);
     }
 }
 
@@ -584,11 +600,14 @@ __host__ __device__ __forceinline__ void pass_step(int k, const PassArgs& a, con
             ntt_step<S, Rd::r0, S, KNZ, INV, true, false, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr);
     } else if (k == 1) {
         if (n == 2)
-            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, tab);
+            ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, true, ROLE, LOGV, pass_streams<KNZ>()>(a, t, l, tid, T,
+                                                                                                   lds, wtab, tab);
         else if (n == 3)
             ntt_step<S, Rd::r1, S - Rd::r0, 8, INV, false, false, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, nullptr);
     } else if (k == 2) {
-        if (n == 3) ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE, LOGV>(a, t, l, tid, T, lds, wtab, tab);
+        if (n == 3)
+            ntt_step<S, Rd::r2, Rd::r2, 8, INV, false, true, ROLE, LOGV, pass_streams<KNZ>()>(a, t, l, tid, T, lds,
+                                                                                              wtab, tab);
     }
 }
 
