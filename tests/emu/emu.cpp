@@ -200,7 +200,7 @@ void emu_p2_permute(uint64_t* st, const uint64_t* rc_init, const uint64_t* rc_fi
         }
     for (int k = 0; k < 22; k++) c.internal[k] = rc_internal[k];
     c.diag15 = diag15;
-    if (fast_diag)
+    if (fast_diag && p2_fast_constants(c))
         p2_permute<true>(st, c);
     else
         p2_permute<false>(st, c);
@@ -307,7 +307,7 @@ int emu_lde_leaf(const uint64_t* in, uint64_t h, uint64_t w, uint32_t log_blowup
         const PassArgs a = pass_args(p, i, B, w, in, h, tmp.data(), out, tab.data(), false);
         if (a.last) {
             if (!last_leaf_fusable(a)) return 1;
-            run_last_leaf(a, digests, n * 8, c, fast_diag != 0);
+            run_last_leaf(a, digests, n * 8, c, fast_diag != 0 && p2_fast_constants(c));
         } else {
             run_pass(a, 512, false);
         }

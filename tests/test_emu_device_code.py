@@ -69,6 +69,28 @@ def test_permutation(emu, oracle, fast):
     assert (s == oracle.p2_permute(np.arange(16, dtype=np.uint64))).all()
 
 
+@pytest.mark.parametrize("big", [0xFFFFFFBFFFFFFFFF, 0xFFFFFFC000000000, 0xFFFFFFFF00000000])
+def test_permutation_constant_bound(emu, oracle, big):
+    """Linear-layer constants at the fast path's bound: just below 2^64 - 2^38
+    the constants join the low sums whole (edge states make those sums as
+    large as they get); at or above it the general path is chosen."""
+    import random
+    rng = random.Random(41)
+    a, b, c, d = oracle.p2_constants()
+    a2, b2, c2 = a.copy(), b.copy(), c.copy()
+    a2[:] = big
+    b2[16:] = big
+    c2[0] = big
+    try:
+        oracle.p2_set_constants(a2, b2, c2, d)
+        for st in _edge_states(rng)[:30]:
+            s = np.array(st, np.uint64)
+            emu.emu_p2_permute(ptr(s), ptr(a2), ptr(b2), ptr(c2), d, 1)
+            assert (s == oracle.p2_permute(np.array([v % P for v in st], np.uint64))).all(), (hex(big), st)
+    finally:
+        oracle.p2_set_constants(a, b, c, d)
+
+
 def _edge_states(rng):
     """States that hit the ends of every lane form: all-ones words, values
     at and above p, halves of 0 and 2^32 - 1, powers of two, random."""

@@ -194,6 +194,31 @@ def test_generic_diag15_path(native, oracle):
     assert (root == oracle.merkle_commit(m)[1]).all()
 
 
+def test_large_round_constants_path(native, oracle):
+    """Linear-layer constants at or above 2^64 - 2^38 (with the default
+    diag15) select the general path, whose constants join as two halves;
+    the default constants are restored afterwards on both sides."""
+    _case("large round constants")
+    a, b, c, d = oracle.p2_constants()
+    a2, b2, c2 = a.copy(), b.copy(), c.copy()
+    a2[5] = 0xFFFFFFFF00000000          # p - 1, in an initial round
+    b2[20] = 0xFFFFFFC000000000         # 2^64 - 2^38, in a terminal round
+    c2[0] = 0xFFFFFFFF00000000          # the first internal round's constant
+    try:
+        oracle.p2_set_constants(a2, b2, c2, d)
+        mmcs = pcs.HipMerkleTreeMmcs((a2, b2, c2, d))
+        m = oracle.gen_uniform(10, 40 * 16).reshape(40, 16)
+        root, _ = mmcs.commit(m)
+        _, oroot = oracle.merkle_commit(m)
+        assert (root == oroot).all()
+    finally:
+        oracle.p2_set_constants(a, b, c, d)
+        pcs.HipMerkleTreeMmcs((a, b, c, d))
+    m = oracle.gen_uniform(10, 40 * 16).reshape(40, 16)
+    root, _ = pcs.HipMerkleTreeMmcs().commit(m)
+    assert (root == oracle.merkle_commit(m)[1]).all()
+
+
 def test_profile_counters(native, oracle):
     _case("profile")
     native.profile_enable(True)

@@ -91,12 +91,13 @@ int upload(const P2Consts& in)
     p2_set_diag(c);
     ZK_TRY(hipMemcpyToSymbol(HIP_SYMBOL(c_p2), &c, sizeof(P2Consts), 0, hipMemcpyHostToDevice));
     g_uploaded[dev] = true;
-    g_diag_fast[dev] = gl_canon(c.diag15) == INV_2_32;
+    g_diag_fast[dev] = p2_fast_constants(c);
     return ZKIE_OK;
 }
 
 // Upload the default constants on first use of a device; report whether
-// the 2^-32 diagonal fast path applies.
+// the fast path applies (2^-32 diagonal, linear-layer constants below
+// kRcLimit: p2_fast_constants).
 int ensure_constants(bool* diag_fast)
 {
     std::lock_guard<std::mutex> g(g_const_mu);

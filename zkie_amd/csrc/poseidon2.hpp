@@ -112,10 +112,13 @@ __host__ __device__ __forceinline__ void mat4_wide(const uint64_t* x, uint64_t* 
 // the other words are left holding their inputs, for a caller that never
 // reads them (the last layer of a permutation whose caller keeps only the
 // digest, or only the capacity before the next absorb overwrites the rate).
+// RC64: every constant is below kRcLimit, so it joins the low sum whole
+// (A < 2^38 there, so A + rc cannot carry) instead of as two halves.
 enum { kRcNone = 0, kRcAll = 1, kRcLane0 = 2 };
 enum { kOutAll = 0xF, kOutDigest = 0x3, kOutCapacity = 0xC };
+constexpr uint64_t kRcLimit = 0xFFFFFFC000000000ull;  // 2^64 - 2^38
 
-template <int RC, int GROUPS = kOutAll>
+template <int RC, int GROUPS = kOutAll, bool RC64 = false>
 __host__ __device__ __forceinline__ void mds_light16_rc(uint64_t* st, const uint64_t* rc)
 {
     uint64_t sl[4], sh[4];
@@ -143,8 +146,12 @@ __host__ __device__ __forceinline__ void mds_light16_rc(uint64_t* st, const uint
         for (int k = 0; k < 4; k++) {
             uint64_t A = yl[k], B = yh[k];
             if (RC == kRcAll || (RC == kRcLane0 && j + k == 0)) {
-                A = acc32s(A, (uint32_t)rc[j + k]);
-                B = acc32s(B, (uint32_t)(rc[j + k] >> 32));
+                if (RC64) {
+                    A += rc[j + k];
+                } else {
+                    A = acc32s(A, (uint32_t)rc[j + k]);
+                    B = acc32s(B, (uint32_t)(rc[j + k] >> 32));
+                }
             }
             st[j + k] = gl_from_halves_defer(A, B, w[j + k]);
         }
@@ -287,18 +294,29 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
     internal_round_core<DIAG15_IS_INV_2_32>(st, 0, diag15);
 }
 
-// OUT: the output words the caller reads (kOutAll, kOutDigest for words
-// 0..7, kOutCapacity for words 8..15), or kOutAbsorb: the caller passes
-// last = whether this is the last absorb of a sponge (digest) or not
-// (capacity), a value uniform over the wave. Words outside OUT are left
-// undefined.
+// FAST: the constant set has diag15 = 2^-32 and every constant that a
+// linear layer adds (ext[0..4), ext[5..8), internal[0]) below kRcLimit
+// (p2_fast_constants); the caller checks this on the host. OUT: the output
+// words the caller reads (kOutAll, kOutDigest for words 0..7, kOutCapacity
+// for words 8..15), or kOutAbsorb: the caller passes last = whether this is
+// the last absorb of a sponge (digest) or not (capacity), a value uniform
+// over the wave. Words outside OUT are left undefined.
 enum { kOutAbsorb = 0 };
 
-template <bool DIAG15_IS_INV_2_32, int OUT = kOutAll>
+inline bool p2_fast_constants(const P2Consts& c)
+{
+    if (gl_canon(c.diag15) != INV_2_32) return false;
+    for (int k = 0; k < 8; k++)
+        for (int i = 0; i < 16; i++)
+            if (k != 4 && c.ext[k][i] >= kRcLimit) return false;
+    return c.internal[0] < kRcLimit;
+}
+
+template <bool FAST, int OUT = kOutAll>
 __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts& C, bool last = true)
 {
     // Initial linear layer fused with the first round's constants.
-    mds_light16_rc<kRcAll>(st, C.ext[0]);
+    mds_light16_rc<kRcAll, kOutAll, FAST>(st, C.ext[0]);
 #pragma unroll 1
     for (int r = 0; r < 8; r++) {
 #pragma unroll
@@ -306,10 +324,10 @@ __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts
         if (r == 3) {
             // the linear layer adds the first internal round's constant to
             // word 0 and every internal round the next one's
-            mds_light16_rc<kRcLane0>(st, C.internal);
+            mds_light16_rc<kRcLane0, kOutAll, FAST>(st, C.internal);
 #pragma unroll 1
             for (int k = 0; k < 22; k++)
-                internal_round_core<DIAG15_IS_INV_2_32>(st, k < 21 ? C.internal[k + 1] : 0, C.diag15);
+                internal_round_core<FAST>(st, k < 21 ? C.internal[k + 1] : 0, C.diag15);
             // constants of the first terminal round (st += rc) before its S-box
 #pragma unroll
             for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
@@ -321,7 +339,7 @@ __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts
             else
                 mds_light16_rc<kRcNone, kOutCapacity>(st, nullptr);
         } else {
-            mds_light16_rc<kRcAll>(st, C.ext[r + 1]);
+            mds_light16_rc<kRcAll, kOutAll, FAST>(st, C.ext[r + 1]);
         }
     }
 }
