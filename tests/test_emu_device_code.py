@@ -79,7 +79,7 @@ def test_permutation_constant_bound(emu, oracle, big):
     a, b, c, d = oracle.p2_constants()
     a2, b2, c2 = a.copy(), b.copy(), c.copy()
     a2[:] = big
-    b2[16:] = big
+    b2[:] = big
     c2[0] = big
     try:
         oracle.p2_set_constants(a2, b2, c2, d)

@@ -213,8 +213,9 @@ __host__ __device__ __forceinline__ void inv_pow2_neg(uint64_t x, uint64_t SL, u
     B = acc32(acc32(SH, m), ~((uint32_t)(q >> 32) + 2u));
 }
 
-template <bool DIAG15_IS_INV_2_32>
-__host__ __device__ __forceinline__ void internal_round_core(uint64_t* st, uint64_t rc0_next, uint64_t diag15)
+template <bool DIAG15_IS_INV_2_32, bool TERM = false>
+__host__ __device__ __forceinline__ void internal_round_core(uint64_t* st, uint64_t rc0_next, uint64_t diag15,
+                                                             const uint64_t* term = nullptr)
 {
     uint64_t SL = (uint32_t)st[1], SH = st[1] >> 32;
 #pragma unroll
@@ -225,9 +226,14 @@ __host__ __device__ __forceinline__ void internal_round_core(uint64_t* st, uint6
     const uint64_t x0 = sbox7(st[0]);
     SL = acc32(SL, (uint32_t)x0);
     SH = acc32(SH, (uint32_t)(x0 >> 32));
-    // the constant added to output i: the next round's rc0 on word 0
-    auto cl = [&](int i) -> uint64_t { return i == 0 ? (uint64_t)(uint32_t)rc0_next : 0; };
-    auto ch = [&](int i) -> uint64_t { return i == 0 ? rc0_next >> 32 : 0; };
+    // the constant added to output i: the next round's rc0 on word 0, or
+    // (TERM, the last internal round on the fast path) the first terminal
+    // round's constant term[i] on every word, whole in the low sum
+    auto cl = [&](int i) -> uint64_t {
+        if (TERM) return term[i];
+        return i == 0 ? (uint64_t)(uint32_t)rc0_next : 0;
+    };
+    auto ch = [&](int i) -> uint64_t { return !TERM && i == 0 ? rc0_next >> 32 : 0; };
     // Each output is finished as soon as its sums are formed (few sums live
     // at once); the rare final folds are applied per group of four words.
     uint64_t w[4];
@@ -238,6 +244,11 @@ __host__ __device__ __forceinline__ void internal_round_core(uint64_t* st, uint6
 #pragma unroll
             for (int i = 0; i < 4; i++) gl_fold_eps(st[j + i], w[i]);
         }
+#if defined(__HIP_DEVICE_COMPILE__)
+        // TERM: the next group's constants are loaded after this point, so
+        // that at most four of them are live at once (scalar registers)
+        if (TERM) asm volatile("" ::: "memory");
+#endif
     };
     uint64_t A, B;
     {
@@ -295,7 +306,7 @@ __host__ __device__ __forceinline__ void internal_round(uint64_t* st, uint64_t r
 }
 
 // FAST: the constant set has diag15 = 2^-32 and every constant that a
-// linear layer adds (ext[0..4), ext[5..8), internal[0]) below kRcLimit
+// linear layer adds (ext[0..8), internal[0]) below kRcLimit
 // (p2_fast_constants); the caller checks this on the host. OUT: the output
 // words the caller reads (kOutAll, kOutDigest for words 0..7, kOutCapacity
 // for words 8..15), or kOutAbsorb: the caller passes last = whether this is
@@ -308,7 +319,7 @@ inline bool p2_fast_constants(const P2Consts& c)
     if (gl_canon(c.diag15) != INV_2_32) return false;
     for (int k = 0; k < 8; k++)
         for (int i = 0; i < 16; i++)
-            if (k != 4 && c.ext[k][i] >= kRcLimit) return false;
+            if (c.ext[k][i] >= kRcLimit) return false;
     return c.internal[0] < kRcLimit;
 }
 
@@ -325,12 +336,20 @@ __host__ __device__ __forceinline__ void p2_permute(uint64_t* st, const P2Consts
             // the linear layer adds the first internal round's constant to
             // word 0 and every internal round the next one's
             mds_light16_rc<kRcLane0, kOutAll, FAST>(st, C.internal);
+            if (FAST) {
+                // the last internal round adds the first terminal round's
+                // constants (st += rc before its S-box) to its sums
 #pragma unroll 1
-            for (int k = 0; k < 22; k++)
-                internal_round_core<FAST>(st, k < 21 ? C.internal[k + 1] : 0, C.diag15);
-            // constants of the first terminal round (st += rc) before its S-box
+                for (int k = 0; k < 21; k++) internal_round_core<FAST>(st, C.internal[k + 1], C.diag15);
+                internal_round_core<FAST, true>(st, 0, C.diag15, C.ext[4]);
+            } else {
+#pragma unroll 1
+                for (int k = 0; k < 22; k++)
+                    internal_round_core<FAST>(st, k < 21 ? C.internal[k + 1] : 0, C.diag15);
+                // constants of the first terminal round (st += rc) before its S-box
 #pragma unroll
-            for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
+                for (int i = 0; i < 16; i++) st[i] = gl_add_small(st[i], C.ext[4][i]);
+            }
         } else if (r == 7) {
             if (OUT != kOutAbsorb)
                 mds_light16_rc<kRcNone, OUT>(st, nullptr);
